@@ -1,0 +1,124 @@
+/*
+ * slipstream_hip.h -- C ABI of the MI355X (gfx950) ragged paged-attention path.
+ *
+ * The shared library libslipstream_hip.so exports exactly the functions below.
+ * Every entry point takes plain device pointers, element counts and element
+ * strides, runs asynchronously on the HIP stream it is given (NULL = default
+ * stream), never synchronises and never frees memory it did not allocate.
+ * Outputs and workspaces are allocated by the caller.
+ *
+ * Return value: SS_OK (0) on success, otherwise one of the SS_ERR_* codes;
+ * ss_status_string() names it and ss_last_error() gives the detail of the
+ * most recent failure on the calling thread.
+ *
+ * Layout contract shared with the caller (reference: slipstream/core/types.py:23-29,
+ * slipstream/memory/paged_cache.py:13-28):
+ *   kv_cache  [num_layers, 2, num_blocks, block_size, num_kv_heads, head_dim]
+ *   slot      = block * block_size + offset           (paged_cache.py:31-32)
+ *   block_tables [batch, max_blocks] int32, -1 padded (paged_cache.py:57-68)
+ *   seq_lens / context_lens [batch] int32: KV length after this step's tokens
+ *   were reserved (paged_cache.py:39-41).
+ * Callers pass the K plane and the V plane of one layer (kv_cache[layer, 0] and
+ * kv_cache[layer, 1]) as two base pointers with one shared set of strides.
+ */
+#ifndef SLIPSTREAM_HIP_H
+#define SLIPSTREAM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SS_OK 0
+#define SS_ERR_INVALID 1     /* argument or shape error (Python raises ValueError)     */
+#define SS_ERR_UNSUPPORTED 2 /* shape/dtype outside the kernels' tiles (RuntimeError)  */
+#define SS_ERR_LAUNCH 3      /* HIP runtime error at launch                            */
+#define SS_ERR_WORKSPACE 4   /* workspace too small                                    */
+
+#define SS_DTYPE_F16 0
+#define SS_DTYPE_BF16 1
+#define SS_DTYPE_F32 2
+
+const char* ss_status_string(int status);
+const char* ss_last_error(void);
+/* Library version, as major*10000 + minor*100 + patch. */
+int ss_version(void);
+
+/*
+ * KV-cache slot-mapping scatter.
+ * Replaces slipstream/kernels/reshape_and_cache.py:10-27 (dispatcher) whose
+ * fast path is reshape_and_cache_triton (slipstream/kernels/triton_paged.py:209-258)
+ * and whose oracle is reshape_and_cache_ref (slipstream/kernels/attention_ref.py:21-39).
+ *
+ * Token n (0 <= n < n_outer*n_inner) is k[n / n_inner, n % n_inner] with head
+ * stride and unit dim stride, i.e. element (n, h, d) lives at
+ *   k + (n / n_inner) * k_strides[0] + (n % n_inner) * k_strides[1] + h * k_strides[2] + d.
+ * ([N, n_kv, D] input: n_outer = 1, n_inner = N; the reference's [B, n_kv, T, D]
+ * input: n_outer = B, n_inner = T, strides (b, t, h) -- no copy is made.)
+ * It is copied bit for bit to k_cache + blk*c_strides[0] + off*c_strides[1] + h*c_strides[2] + d
+ * with blk = slot / block_size, off = slot % block_size, slot = slot_mapping[n].
+ * Slots < 0 are skipped (triton_paged.py:70-71); slots >= num_slots are skipped
+ * as well, so a bad slot never writes outside the pool.
+ * elem_bytes is 2 (fp16/bf16) or 4 (fp32); strides are in elements.
+ */
+int ss_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_cache,
+                         const int64_t* slot_mapping, int64_t n_outer, int64_t n_inner,
+                         int n_kv, int head_dim, int block_size, int64_t num_slots,
+                         const int64_t k_strides[3], const int64_t v_strides[3],
+                         const int64_t c_strides[3], int elem_bytes, void* stream);
+
+/*
+ * Paged attention over block tables, padded form [B, n_q, Tq, D].
+ * Replaces paged_attention_decode (slipstream/kernels/paged_attention.py:21-40)
+ * and paged_attention_prefill (paged_attention.py:43-52); semantics of
+ * paged_attention_ref (attention_ref.py:68-89) with eager_attention
+ * (slipstream/models/layers/attention.py:64-88) and the edge rules of the Triton
+ * kernel (triton_paged.py:133-206): query j of sequence b sits at absolute
+ * position seq_lens[b] - Tq + j and sees keys [0, seq_lens[b] - Tq + j];
+ * KV head of query head h is h / (n_q / n_kv); table entries < 0 (or >= num_blocks)
+ * are masked; a query row with no visible key outputs zeros.
+ *
+ * q(b, h, t, d)   = q   + b*q_strides[0] + h*q_strides[1] + t*q_strides[2] + d
+ * out(b, t, h, d) = out + b*o_strides[0] + t*o_strides[1] + h*o_strides[2] + d
+ * cache element (blk, off, h, d) = cache + blk*c_strides[0] + off*c_strides[1] + h*c_strides[2] + d
+ * block_tables(b, i) = block_tables[b * bt_stride + i]
+ * dtype: SS_DTYPE_BF16 or SS_DTYPE_F16 (q, cache and out share it).
+ * workspace: device scratch of at least ss_paged_attention_workspace_size() bytes.
+ */
+int ss_paged_attention_workspace_size(int64_t batch, int n_q, int n_kv, int head_dim,
+                                      int max_query_len, int dtype, int64_t* bytes);
+
+int ss_paged_attention(const void* q, void* out, const void* k_cache, const void* v_cache,
+                       const int32_t* block_tables, const int32_t* seq_lens, int64_t batch,
+                       int n_q, int n_kv, int head_dim, int tq, int max_blocks, int block_size,
+                       int64_t num_blocks, const int64_t q_strides[3], const int64_t o_strides[3],
+                       const int64_t c_strides[3], int64_t bt_stride, float scale, int dtype,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Packed (varlen) paged attention: one token stream q [T, n_q, D] holding the
+ * query tokens of all sequences back to back; sequence b owns tokens
+ * [cu_seqlens[b], cu_seqlens[b+1]) and has context_lens[b] KV tokens after this
+ * step's tokens were written. The reference has no packed entry: its engine
+ * runs decodes as B x 1 (llm_engine.py:540-567) and each prefill chunk as its own
+ * B = 1 call (llm_engine.py:508-538); this entry equals those per-sequence calls
+ * concatenated. Rows with one query token per KV head group small enough for
+ * the decode tile take the split-K decode kernel, the others the MFMA prefill
+ * kernel, both inside this call.
+ * q(t, h, d) = q + t*q_strides[0] + h*q_strides[1] + d; out likewise with o_strides.
+ */
+int ss_paged_attention_varlen(const void* q, void* out, const void* k_cache, const void* v_cache,
+                              const int32_t* block_tables, const int32_t* cu_seqlens,
+                              const int32_t* context_lens, int64_t batch, int64_t total_tokens,
+                              int n_q, int n_kv, int head_dim, int max_query_len, int max_blocks,
+                              int block_size, int64_t num_blocks, const int64_t q_strides[2],
+                              const int64_t o_strides[2], const int64_t c_strides[3],
+                              int64_t bt_stride, float scale, int dtype, void* workspace,
+                              int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SLIPSTREAM_HIP_H */

@@ -1,0 +1,76 @@
+// Parameters and per-sequence metadata shared by the paged-attention kernels.
+#pragma once
+
+#include "ss_common.h"
+
+namespace ss {
+
+// Everything a paged-attention launch needs. Pointers are raw device pointers,
+// strides are in elements. A sequence ("row" of the batch) b owns query tokens
+// [qoff(b), qoff(b) + qlen(b)) and ctx(b) KV tokens reached through
+// block_tables[b * bt_stride + i].
+struct AttnParams {
+  const void* q;
+  void* out;
+  const void* kc;  // K plane of the layer: [num_blocks, block_size, n_kv, D]
+  const void* vc;  // V plane of the layer, same strides
+  const int32_t* bt;
+  const int32_t* ctx_lens;  // seq_lens / context_lens [batch]
+  const int32_t* cu;        // cu_seqlens [batch+1] for the packed form, nullptr when padded
+  int64_t q_sb, q_st, q_sh;  // padded: (b, t, h); packed: q_sb = 0, q_st = token stride
+  int64_t o_sb, o_st, o_sh;
+  int64_t c_sb, c_so, c_sh;  // cache strides (block, offset, head)
+  int64_t bt_stride;
+  int64_t num_blocks;
+  int batch, n_q, n_kv, n_rep;
+  int tq;  // padded query length (unused when cu != nullptr)
+  int max_blocks, bs_shift, block_size;
+  float scale_log2;  // softmax scale * log2(e)
+  // split-K decode bookkeeping (workspace carve-up)
+  float* ws_o;   // [n_wg * 2 * hpw * rmax * D] unnormalised partial outputs
+  float* ws_ml;  // [n_wg * 2 * hpw * rmax * 2]   (running max, running sum)
+  int* ws_rec;   // [n_wg * 8] per-workgroup record of the split sequence it owns
+  int n_ranges;          // work ranges of the decode stream-K partition
+  int hpw;               // KV heads per decode workgroup (one wave each)
+  int n_hgroups;         // n_kv / hpw
+  int rmax;              // query rows per (sequence, KV head) stored in a partial
+};
+
+// Decode tile: one wave covers up to 16 query rows (query token j, head i in
+// the GQA group) of one KV head; r = j * n_rep + i.
+constexpr int kDecodeRows = 16;
+// Keys per decode iteration: two 16-token MFMA tiles.
+constexpr int kPairTokens = 32;
+
+__device__ __forceinline__ void seq_queries(const AttnParams& p, int b, int& qlen, int64_t& qoff) {
+  if (p.cu) {
+    const int s = p.cu[b];
+    qlen = p.cu[b + 1] - s;
+    qoff = s;
+  } else {
+    qlen = p.tq;
+    qoff = 0;
+  }
+}
+
+// KV tokens reachable through the table (Triton: n_blocks = min(cdiv(len, bs), max_blocks)).
+__device__ __forceinline__ int seq_kv_tokens(const AttnParams& p, int ctx) {
+  const int cap = p.max_blocks << p.bs_shift;
+  ctx = ctx < 0 ? 0 : ctx;
+  return ctx < cap ? ctx : cap;
+}
+
+// Sequences whose qlen * n_rep query rows fit the decode tile (p.rmax <= 16 rows,
+// set per launch from max_query_len) take the split-K decode kernel; the rest
+// take the prefill kernel. Both kernels use this one predicate.
+__device__ __forceinline__ bool is_decode_seq(const AttnParams& p, int qlen) {
+  return qlen >= 1 && qlen * p.n_rep <= p.rmax;
+}
+
+// rmax for a launch whose longest query is max_query_len.
+inline int decode_rows_for(int max_query_len, int n_rep) {
+  long long r = (long long)(max_query_len < 1 ? 1 : max_query_len) * n_rep;
+  return r > kDecodeRows ? kDecodeRows : (int)r;
+}
+
+}  // namespace ss

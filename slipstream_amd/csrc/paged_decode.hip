@@ -1,0 +1,524 @@
+// Split-K paged-attention decode for gfx950.
+//
+// Math (slipstream/models/layers/attention.py:64-88 via
+// slipstream/kernels/attention_ref.py:68-89, edge rules of
+// slipstream/kernels/triton_paged.py:133-206): for query row r = (token j, head
+// i of the GQA group of KV head h) of sequence b,
+//   out = softmax(scale * q . K^T + causal) . V
+// over the first ctx(b) tokens gathered through block_tables[b].
+//
+// Work partition ("stream-K"): the decode sequences' KV is cut into pairs of
+// 16-token tiles (32 keys). All pairs of all sequences form one list, in
+// sequence order; workgroup w takes the contiguous range
+// [w*chunk, (w+1)*chunk). A workgroup has one wavefront per KV head of its head
+// group, so its waves stream the same pages of the same blocks (contiguous
+// [block, offset, head, d] memory). A sequence finished inside one range is
+// written directly; a sequence cut by a range boundary leaves an unnormalised
+// partial (max, sum, acc) per range, and the merge kernel combines them. Every
+// workgroup gets the same number of pairs, whatever the length distribution.
+//
+// Per wavefront and pair:
+//   S^T = K Q^T   : 2 tiles x D/32 MFMA 16x16x32 (A = K rows straight from
+//                   HBM in MFMA layout, B = Q^T held in registers)
+//   online softmax in fp32 (exp2 domain), max across the 4 lane rows with
+//                   v_permlane{16,32}_swap
+//   O^T += V^T P^T: D/8/16 x 8 MFMA; V is loaded as whole 256-byte rows (each
+//                   lane 8 tokens x 8 consecutive d) and transposed inside the
+//                   lane with v_perm_b32, because MFMA row m of product i stands
+//                   for d = 8*m + i. P^T comes straight out of the S^T
+//                   accumulator layout. No LDS is used.
+#include "attention_common.h"
+
+namespace ss {
+namespace {
+
+// Target of every load for an absent key (past the context, or in a block whose
+// table entry is negative or out of range). Never written, so it stays zero.
+__device__ __attribute__((aligned(16))) uint32_t g_zero_row[128];
+
+__device__ __forceinline__ int block_sum(int v, int* sh) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) sh[wave] = v;
+  __syncthreads();
+  int t = 0;
+  for (int i = 0; i < nw; ++i) t += sh[i];
+  return t;
+}
+
+__device__ __forceinline__ int block_incl_scan(int v, int* sh, int& total) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(v, o);
+    if (lane >= o) v += u;
+  }
+  __syncthreads();
+  if (lane == 63) sh[wave] = v;
+  __syncthreads();
+  int pre = 0;
+  total = 0;
+  for (int i = 0; i < nw; ++i) {
+    const int s = sh[i];
+    if (i < wave) pre += s;
+    total += s;
+  }
+  return v + pre;
+}
+
+// Pairs of 16-token tiles the decode kernel owns for sequence b (0 for
+// sequences left to the prefill kernel or with nothing to attend to).
+__device__ __forceinline__ int decode_pairs(const AttnParams& p, int b) {
+  int qlen;
+  int64_t qoff;
+  seq_queries(p, b, qlen, qoff);
+  if (!is_decode_seq(p, qlen)) return 0;
+  const int kvt = seq_kv_tokens(p, p.ctx_lens[b]);
+  return (kvt + kPairTokens - 1) / kPairTokens;
+}
+
+template <typename T, int D>
+struct DecodeTile {
+  static constexpr int NCH = D / 8;             // 16-byte chunks in a head row
+  static constexpr int MT = (NCH + 15) / 16;    // PV product sets (16 chunks each)
+  static constexpr int KS = D / 32;             // QK k-steps
+  u32x4 k[2][KS];   // A operands of S^T: row = token (lane & 15), k = d
+  u32x4 v[MT][8];   // 8 tokens of lane row g x 8 consecutive d of chunk (lane & 15) + 16*mt
+  int valid;        // bit x: tile x of this lane row's V tokens lives in a valid block
+};
+
+// Issue the loads of pair `pi` of the sequence whose table is `table`.
+// Every load is unconditional: absent keys read the zero row instead.
+template <typename T, int D>
+__device__ __forceinline__ void load_pair(const AttnParams& p, const int32_t* table, int kvt, int pi,
+                                          int h, int lane, DecodeTile<T, D>& t) {
+  typedef DecodeTile<T, D> Tile;
+  const char* kc = (const char*)p.kc;
+  const char* vc = (const char*)p.vc;
+  const char* zero = (const char*)g_zero_row;
+  const int n = lane & 15, g = lane >> 4;
+  const int bmask = p.block_size - 1;
+  const int64_t hoff = (int64_t)h * p.c_sh;
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    // K: this lane's token is n of tile x
+    const int tk = pi * kPairTokens + 16 * x + n;
+    int bi = tk >> p.bs_shift;
+    bi = bi < p.max_blocks ? bi : p.max_blocks - 1;
+    const int phys = table[bi];
+    const bool ok = tk < kvt && phys >= 0 && phys < p.num_blocks;
+    const char* krow =
+        ok ? kc + ((int64_t)phys * p.c_sb + (int64_t)(tk & bmask) * p.c_so + hoff) * (int64_t)sizeof(T)
+           : zero;
+#pragma unroll
+    for (int s = 0; s < Tile::KS; ++s) t.k[x][s] = load16(krow + (32 * s + 8 * g) * (int)sizeof(T));
+  }
+  t.valid = 0;
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    // V: tokens 4g..4g+3 of tile x share one block (block_size >= 4)
+    const int t0 = pi * kPairTokens + 16 * x + 4 * g;
+    int bi = t0 >> p.bs_shift;
+    bi = bi < p.max_blocks ? bi : p.max_blocks - 1;
+    const int phys = table[bi];
+    const bool okb = phys >= 0 && phys < p.num_blocks;
+    if (okb) t.valid |= 1 << x;
+    const int64_t base = ((int64_t)phys * p.c_sb + hoff) * (int64_t)sizeof(T);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int tv = t0 + e;
+      const char* vrow = (okb && tv < kvt) ? vc + base + (int64_t)(tv & bmask) * p.c_so * (int64_t)sizeof(T)
+                                           : zero;
+#pragma unroll
+      for (int mt = 0; mt < Tile::MT; ++mt) {
+        const int cc = n + 16 * mt;
+        const int ccl = cc < Tile::NCH ? cc : 0;
+        t.v[mt][4 * x + e] = load16(vrow + 8 * ccl * (int)sizeof(T));
+      }
+    }
+  }
+}
+
+template <typename T, int D>
+struct RowState {
+  static constexpr int NACC = DecodeTile<T, D>::MT * 8;
+  f32x4 acc[NACC];  // acc[mt*8+i][e] = O[row][128*mt + 32*g + 8*e + i]
+  float m;          // running max (log2 domain), uniform over the lanes of a row
+  float l;          // this lane's partial sum of exp2(s - m)
+};
+
+template <typename T, int D>
+__device__ __forceinline__ void compute_pair(const AttnParams& p, const DecodeTile<T, D>& t,
+                                             const u32x4 (&qop)[D / 32], int pi, int lim_eff, int lane,
+                                             RowState<T, D>& st) {
+  typedef DecodeTile<T, D> Tile;
+  const int g = lane >> 4;
+  f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < Tile::KS; ++s) {
+    s0 = Elem<T>::mfma(t.k[0][s], qop[s], s0);
+    s1 = Elem<T>::mfma(t.k[1][s], qop[s], s1);
+  }
+  // s0[e] = S[token pi*32 + 4g + e][row], s1[e] = S[token pi*32 + 16 + 4g + e][row]
+  float sv[8];
+  const int tb = pi * kPairTokens + 4 * g;
+  const float ninf = -__builtin_inff();
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    sv[e] = ((t.valid & 1) && tb + e < lim_eff) ? s0[e] * p.scale_log2 : ninf;
+    sv[4 + e] = ((t.valid & 2) && tb + 16 + e < lim_eff) ? s1[e] * p.scale_log2 : ninf;
+  }
+  float mx = sv[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
+  mx = max_across_rows(mx);
+  const float mnew = fmaxf(st.m, mx);
+  const float alpha = fast_exp2(st.m - mnew);
+  float pv[8];
+  float ps = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    pv[e] = fast_exp2(sv[e] - mnew);
+    ps += pv[e];
+  }
+  st.l = st.l * alpha + ps;
+  st.m = mnew;
+  const u32x4 pop = {Elem<T>::pack2(pv[0], pv[1]), Elem<T>::pack2(pv[2], pv[3]),
+                     Elem<T>::pack2(pv[4], pv[5]), Elem<T>::pack2(pv[6], pv[7])};
+#pragma unroll
+  for (int a = 0; a < RowState<T, D>::NACC; ++a) st.acc[a] *= alpha;
+#pragma unroll
+  for (int mt = 0; mt < Tile::MT; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      u32x4 a;
+      if (i & 1) {
+        a[0] = pick_halves<1, 1>(t.v[mt][0][i >> 1], t.v[mt][1][i >> 1]);
+        a[1] = pick_halves<1, 1>(t.v[mt][2][i >> 1], t.v[mt][3][i >> 1]);
+        a[2] = pick_halves<1, 1>(t.v[mt][4][i >> 1], t.v[mt][5][i >> 1]);
+        a[3] = pick_halves<1, 1>(t.v[mt][6][i >> 1], t.v[mt][7][i >> 1]);
+      } else {
+        a[0] = pick_halves<0, 0>(t.v[mt][0][i >> 1], t.v[mt][1][i >> 1]);
+        a[1] = pick_halves<0, 0>(t.v[mt][2][i >> 1], t.v[mt][3][i >> 1]);
+        a[2] = pick_halves<0, 0>(t.v[mt][4][i >> 1], t.v[mt][5][i >> 1]);
+        a[3] = pick_halves<0, 0>(t.v[mt][6][i >> 1], t.v[mt][7][i >> 1]);
+      }
+      st.acc[mt * 8 + i] = Elem<T>::mfma(a, pop, st.acc[mt * 8 + i]);
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
+  typedef DecodeTile<T, D> Tile;
+  __shared__ int s_red[16];
+  __shared__ int s_b0, s_c0;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int hg = blockIdx.x % p.n_hgroups;
+  const int wr = blockIdx.x / p.n_hgroups;
+  const int h = hg * p.hpw + wave;
+  int* rec = p.ws_rec + (int64_t)blockIdx.x * 8;
+
+  // ---- plan: total pairs, this range, and the sequence holding its first pair
+  int local = 0;
+  for (int b = tid; b < p.batch; b += blockDim.x) local += decode_pairs(p, b);
+  const int total = block_sum(local, s_red);
+  const int chunk = (total + p.n_ranges - 1) / p.n_ranges;
+  const int s_w = wr * chunk;
+  const int e_w = min(s_w + chunk, total);
+  if (s_w >= e_w) {
+    if (tid == 0) rec[0] = -1;
+    return;
+  }
+  if (tid == 0) s_b0 = -1;
+  int run = 0;
+  for (int base = 0; base < p.batch; base += blockDim.x) {
+    const int b = base + tid;
+    const int v = b < p.batch ? decode_pairs(p, b) : 0;
+    int tot;
+    const int incl = block_incl_scan(v, s_red, tot);
+    const int cb = run + incl - v;
+    if (v > 0 && cb <= s_w && s_w < cb + v) {
+      s_b0 = b;
+      s_c0 = cb;
+    }
+    run += tot;
+    __syncthreads();
+    if (s_b0 >= 0) break;
+  }
+  int b = s_b0, c = s_c0, pos = s_w;
+  int rec_b = -1, rec_cb = 0, rec_cb1 = 0, rec_slot = 0;
+
+  while (pos < e_w && b < p.batch) {
+    int qlen;
+    int64_t qoff;
+    seq_queries(p, b, qlen, qoff);
+    const int nbp = decode_pairs(p, b);
+    if (nbp == 0) {
+      ++b;
+      continue;
+    }
+    const int seg0 = pos - c;
+    const int seg1 = min(e_w - c, nbp);
+    const int ctx = p.ctx_lens[b] < 0 ? 0 : p.ctx_lens[b];
+    const int kvt = seq_kv_tokens(p, ctx);
+    const int R = qlen * p.n_rep;
+    const bool row_ok = n < R;
+    const int j = row_ok ? n / p.n_rep : 0;
+    const int hq = h * p.n_rep + (row_ok ? n - j * p.n_rep : 0);
+    const int lim = row_ok ? ctx - qlen + j + 1 : 0;
+    const int lim_eff = lim < kvt ? lim : kvt;
+    const T* qrow = (const T*)p.q + (int64_t)b * p.q_sb + (qoff + j) * p.q_st + (int64_t)hq * p.q_sh;
+    u32x4 qop[Tile::KS];
+#pragma unroll
+    for (int s = 0; s < Tile::KS; ++s) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      qop[s] = row_ok ? load16(qrow + 32 * s + 8 * g) : z;
+    }
+    const int32_t* table = p.bt + (int64_t)b * p.bt_stride;
+
+    RowState<T, D> st;
+#pragma unroll
+    for (int a = 0; a < RowState<T, D>::NACC; ++a) st.acc[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m = kNegBig;
+    st.l = 0.f;
+
+    // two-stage software pipeline: loads of pair pi+1 are in flight while pair pi computes
+    DecodeTile<T, D> ta, tb;
+    load_pair<T, D>(p, table, kvt, seg0, h, lane, ta);
+    int pi = seg0;
+    while (true) {
+      load_pair<T, D>(p, table, kvt, pi + 1, h, lane, tb);
+      compute_pair<T, D>(p, ta, qop, pi, lim_eff, lane, st);
+      if (++pi >= seg1) break;
+      load_pair<T, D>(p, table, kvt, pi + 1, h, lane, ta);
+      compute_pair<T, D>(p, tb, qop, pi, lim_eff, lane, st);
+      if (++pi >= seg1) break;
+    }
+
+    const float lt = sum_across_rows(st.l);
+    const bool complete = seg0 == 0 && seg1 == nbp;
+    if (complete) {
+      if (row_ok) {
+        const float inv = lt > 0.f ? 1.f / lt : 0.f;
+        T* orow = (T*)p.out + (int64_t)b * p.o_sb + (qoff + j) * p.o_st + (int64_t)hq * p.o_sh;
+#pragma unroll
+        for (int mt = 0; mt < Tile::MT; ++mt) {
+          const int dbase = 128 * mt + 32 * g;
+          if (dbase < D) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const f32x4* a = &st.acc[mt * 8];
+              const u32x4 o = {Elem<T>::pack2(a[0][e] * inv, a[1][e] * inv),
+                               Elem<T>::pack2(a[2][e] * inv, a[3][e] * inv),
+                               Elem<T>::pack2(a[4][e] * inv, a[5][e] * inv),
+                               Elem<T>::pack2(a[6][e] * inv, a[7][e] * inv)};
+              store16(orow + dbase + 8 * e, o);
+            }
+          }
+        }
+      }
+    } else {
+      const int slot = c > s_w ? 1 : 0;
+      const int64_t pidx = (((int64_t)blockIdx.x * 2 + slot) * p.hpw + wave) * p.rmax + n;
+      if (row_ok) {
+        float* po = p.ws_o + pidx * D;
+#pragma unroll
+        for (int mt = 0; mt < Tile::MT; ++mt) {
+          const int dbase = 128 * mt + 32 * g;
+          if (dbase < D) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const f32x4* a = &st.acc[mt * 8];
+              const f32x4 lo = {a[0][e], a[1][e], a[2][e], a[3][e]};
+              const f32x4 hi = {a[4][e], a[5][e], a[6][e], a[7][e]};
+              *reinterpret_cast<f32x4*>(po + dbase + 8 * e) = lo;
+              *reinterpret_cast<f32x4*>(po + dbase + 8 * e + 4) = hi;
+            }
+          }
+        }
+        if (g == 0) {
+          p.ws_ml[pidx * 2] = st.m;
+          p.ws_ml[pidx * 2 + 1] = lt;
+        }
+      }
+      if (c >= s_w) {
+        rec_b = b;
+        rec_cb = c;
+        rec_cb1 = c + nbp;
+        rec_slot = slot;
+      }
+    }
+    pos = c + seg1;
+    c += nbp;
+    ++b;
+  }
+  if (tid == 0) {
+    rec[0] = rec_b;
+    rec[1] = rec_cb;
+    rec[2] = rec_cb1;
+    rec[3] = rec_slot;
+    rec[4] = chunk;
+  }
+}
+
+// Combine the partials of every sequence cut by a range boundary (blocks
+// [0, n_wg)), and write zeros for decode sequences with no visible key
+// (blocks [n_wg, n_wg + batch)).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void decode_merge_kernel(const AttnParams p, int n_wg) {
+  const int tid = threadIdx.x;
+  if ((int)blockIdx.x >= n_wg) {
+    const int b = blockIdx.x - n_wg;
+    int qlen;
+    int64_t qoff;
+    seq_queries(p, b, qlen, qoff);
+    if (!is_decode_seq(p, qlen) || decode_pairs(p, b) != 0) return;
+    const int64_t per_tok = (int64_t)p.n_q * D;
+    for (int64_t idx = tid; idx < (int64_t)qlen * per_tok; idx += blockDim.x) {
+      const int j = (int)(idx / per_tok);
+      const int rem = (int)(idx - (int64_t)j * per_tok);
+      const int hq = rem / D, d = rem - hq * D;
+      T* o = (T*)p.out + (int64_t)b * p.o_sb + (qoff + j) * p.o_st + (int64_t)hq * p.o_sh + d;
+      *o = (T)0.f;
+    }
+    return;
+  }
+  const int* rec = p.ws_rec + (int64_t)blockIdx.x * 8;
+  const int b = rec[0];
+  if (b < 0) return;
+  const int cb1 = rec[2], slot0 = rec[3], chunk = rec[4];
+  const int hg = blockIdx.x % p.n_hgroups;
+  const int wr0 = blockIdx.x / p.n_hgroups;
+  const int wr1 = (cb1 - 1) / chunk;
+  int qlen;
+  int64_t qoff;
+  seq_queries(p, b, qlen, qoff);
+  const int R = qlen * p.n_rep;
+  const int per_head = R * D;
+  for (int idx = tid; idx < p.hpw * per_head; idx += blockDim.x) {
+    const int wave = idx / per_head;
+    const int r = (idx - wave * per_head) / D;
+    const int d = idx - wave * per_head - r * D;
+    float mmax = kNegBig;
+    for (int wr = wr0; wr <= wr1; ++wr) {
+      const int slot = wr == wr0 ? slot0 : 0;
+      const int64_t pidx = (((int64_t)(wr * p.n_hgroups + hg) * 2 + slot) * p.hpw + wave) * p.rmax + r;
+      mmax = fmaxf(mmax, p.ws_ml[pidx * 2]);
+    }
+    float lsum = 0.f, osum = 0.f;
+    for (int wr = wr0; wr <= wr1; ++wr) {
+      const int slot = wr == wr0 ? slot0 : 0;
+      const int64_t pidx = (((int64_t)(wr * p.n_hgroups + hg) * 2 + slot) * p.hpw + wave) * p.rmax + r;
+      const float f = fast_exp2(p.ws_ml[pidx * 2] - mmax);
+      lsum += p.ws_ml[pidx * 2 + 1] * f;
+      osum += p.ws_o[pidx * D + d] * f;
+    }
+    const int j = r / p.n_rep;
+    const int hq = (hg * p.hpw + wave) * p.n_rep + (r - j * p.n_rep);
+    T* o = (T*)p.out + (int64_t)b * p.o_sb + (qoff + j) * p.o_st + (int64_t)hq * p.o_sh + d;
+    *o = (T)(lsum > 0.f ? osum / lsum : 0.f);
+  }
+}
+
+}  // namespace
+
+// ---- host side -------------------------------------------------------------
+
+static int heads_per_wg(int n_kv) {
+  for (int d = 8; d >= 1; --d)
+    if (n_kv % d == 0) return d;
+  return 1;
+}
+
+template <typename T, int D>
+static int decode_resident_wgs(int hpw) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<T, D>, hpw * 64, 0) !=
+          hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  return per_cu * ss_host::device_cu_count();
+}
+
+// Decode split-K geometry: number of workgroups and bytes of workspace.
+struct DecodeGeometry {
+  int hpw, n_hgroups, n_ranges, n_wg, rmax;
+  int64_t rec_bytes, ml_bytes, o_bytes;
+  int64_t total() const { return rec_bytes + ml_bytes + o_bytes; }
+};
+
+template <typename T, int D>
+static DecodeGeometry decode_geometry(int n_kv, int rmax) {
+  DecodeGeometry g;
+  g.hpw = heads_per_wg(n_kv);
+  g.n_hgroups = n_kv / g.hpw;
+  const int resident = decode_resident_wgs<T, D>(g.hpw);
+  g.n_ranges = resident / g.n_hgroups;
+  if (g.n_ranges < 1) g.n_ranges = 1;
+  g.n_wg = g.n_ranges * g.n_hgroups;
+  g.rmax = rmax;
+  g.rec_bytes = (int64_t)g.n_wg * 8 * 4;
+  g.ml_bytes = (int64_t)g.n_wg * 2 * g.hpw * rmax * 2 * 4;
+  g.o_bytes = (int64_t)g.n_wg * 2 * g.hpw * rmax * D * 4;
+  return g;
+}
+
+static DecodeGeometry geometry_for(int dtype, int head_dim, int n_kv, int rmax) {
+  if (dtype == SS_DTYPE_BF16) {
+    if (head_dim == 64) return decode_geometry<bf16_t, 64>(n_kv, rmax);
+    if (head_dim == 128) return decode_geometry<bf16_t, 128>(n_kv, rmax);
+    return decode_geometry<bf16_t, 256>(n_kv, rmax);
+  }
+  if (head_dim == 64) return decode_geometry<f16_t, 64>(n_kv, rmax);
+  if (head_dim == 128) return decode_geometry<f16_t, 128>(n_kv, rmax);
+  return decode_geometry<f16_t, 256>(n_kv, rmax);
+}
+
+// Bytes the decode part needs for a launch whose longest query is max_query_len.
+int64_t decode_workspace_bytes(int dtype, int head_dim, int n_q, int n_kv, int max_query_len) {
+  return geometry_for(dtype, head_dim, n_kv, decode_rows_for(max_query_len, n_q / n_kv)).total();
+}
+
+template <typename T, int D>
+static int launch_decode_typed(AttnParams p, int max_query_len, char* ws, int64_t ws_bytes,
+                               hipStream_t stream) {
+  const DecodeGeometry g = decode_geometry<T, D>(p.n_kv, decode_rows_for(max_query_len, p.n_rep));
+  if (ws_bytes < g.total()) {
+    ss_host::set_error("paged attention: workspace of %lld bytes, decode needs %lld", (long long)ws_bytes,
+                       (long long)g.total());
+    return SS_ERR_WORKSPACE;
+  }
+  // carve: [rec][ml][o]
+  p.ws_rec = (int*)ws;
+  p.ws_ml = (float*)(ws + g.rec_bytes);
+  p.ws_o = (float*)(ws + g.rec_bytes + g.ml_bytes);
+  p.hpw = g.hpw;
+  p.n_hgroups = g.n_hgroups;
+  p.n_ranges = g.n_ranges;
+  if (p.rmax != g.rmax) {
+    ss_host::set_error("paged attention: decode row split %d != geometry %d", p.rmax, g.rmax);
+    return SS_ERR_INVALID;
+  }
+  hipLaunchKernelGGL((decode_kernel<T, D>), dim3(g.n_wg), dim3(g.hpw * 64), 0, stream, p);
+  int st = ss_host::launch_status("paged attention decode");
+  if (st != SS_OK) return st;
+  hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(g.n_wg + p.batch), dim3(256), 0, stream, p, g.n_wg);
+  return ss_host::launch_status("paged attention decode merge");
+}
+
+int launch_decode(const AttnParams& p, int dtype, int head_dim, int max_query_len, char* ws,
+                  int64_t ws_bytes, hipStream_t stream) {
+  if (dtype == SS_DTYPE_BF16) {
+    if (head_dim == 64) return launch_decode_typed<bf16_t, 64>(p, max_query_len, ws, ws_bytes, stream);
+    if (head_dim == 128) return launch_decode_typed<bf16_t, 128>(p, max_query_len, ws, ws_bytes, stream);
+    return launch_decode_typed<bf16_t, 256>(p, max_query_len, ws, ws_bytes, stream);
+  }
+  if (head_dim == 64) return launch_decode_typed<f16_t, 64>(p, max_query_len, ws, ws_bytes, stream);
+  if (head_dim == 128) return launch_decode_typed<f16_t, 128>(p, max_query_len, ws, ws_bytes, stream);
+  return launch_decode_typed<f16_t, 256>(p, max_query_len, ws, ws_bytes, stream);
+}
+
+}  // namespace ss

@@ -1,0 +1,67 @@
+"""The C-ABI library loads and exports every function ``include/*.h`` declares (no GPU needed)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions() -> list[str]:
+    names: list[str] = []
+    for header in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ss_\w+)\s*\(", text, flags=re.M)
+    return names
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for required in ("ss_reshape_and_cache", "ss_paged_attention", "ss_paged_attention_varlen",
+                     "ss_paged_attention_workspace_size", "ss_status_string", "ss_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    from slipstream_amd import _ffi
+
+    lib = _ffi.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+        assert name in _ffi.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_status_strings_without_gpu():
+    from slipstream_amd import _ffi
+
+    lib = _ffi.lib()
+    assert lib.ss_status_string(0) == b"ok"
+    assert b"invalid" in lib.ss_status_string(1)
+    assert lib.ss_version() >= 100
+
+
+def test_argument_errors_need_no_device():
+    """Shape checks run on the host before any HIP call; a GQA error is SS_ERR_INVALID."""
+    from slipstream_amd import _ffi
+
+    lib = _ffi.lib()
+    z = _ffi.i64_array([0, 0, 0])
+    st = lib.ss_paged_attention(None, None, None, None, None, None, 1, 6, 4, 128, 1, 1, 16, 1,
+                                z, z, z, 0, 1.0, _ffi.SS_DTYPE_BF16, None, 0, None)
+    assert st == _ffi.SS_ERR_INVALID
+    assert b"GQA" in lib.ss_last_error()
+    st = lib.ss_paged_attention(None, None, None, None, None, None, 1, 8, 8, 96, 1, 1, 16, 1,
+                                z, z, z, 0, 1.0, _ffi.SS_DTYPE_BF16, None, 0, None)
+    assert st == _ffi.SS_ERR_UNSUPPORTED
+    with pytest.raises(ValueError):
+        _ffi.check(_ffi.SS_ERR_INVALID, "probe")
+    with pytest.raises(RuntimeError):
+        _ffi.check(_ffi.SS_ERR_UNSUPPORTED, "probe")
+    # empty work is a no-op that touches no pointer
+    st = lib.ss_reshape_and_cache(None, None, None, None, None, 0, 0, 8, 128, 16, 0, z, z, z, 2, None)
+    assert st == _ffi.SS_OK
+    assert isinstance(ctypes.c_int(st).value, int)

@@ -1,0 +1,316 @@
+"""GPU parity of the HIP scatter and paged attention against the numpy oracle.
+
+Every test builds seeded inputs (on the host when they are small, so the
+oracle sees the identical bits), runs the HIP path through the C ABI, and
+compares: the scatter bit for bit, attention within 2e-3 abs + 1e-2 rel.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_attention as ora
+from slipstream_amd import workloads
+from slipstream_amd.kernels import (
+    paged_attention_decode,
+    paged_attention_prefill,
+    paged_attention_varlen,
+    reshape_and_cache,
+)
+from tests._helpers import assert_attn_close, bits, f64, gather_pool_f64, tables_array
+
+pytestmark = pytest.mark.gpu
+
+
+def _to(batch: workloads.PagedBatch, device) -> workloads.PagedBatch:
+    for name in ("kv_cache", "block_tables", "context_lens", "cu_seqlens", "q", "k_new", "v_new",
+                 "slot_mapping"):
+        setattr(batch, name, getattr(batch, name).to(device))
+    return batch
+
+
+def _oracle_padded(batch: workloads.PagedBatch) -> np.ndarray:
+    kv = f64(batch.kv_cache)
+    tables = tables_array(batch.tables_host, batch.block_tables.shape[1])
+    q = f64(batch.padded_q())
+    return ora.paged_attention(q, kv, tables, np.array(batch.ctx_host), 0, batch.scale, batch.block_size)
+
+
+# ---------------------------------------------------------------- scatter
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("layout", ["flat", "bnhd"])
+def test_scatter_bit_exact(device, dtype, layout):
+    print(f"scatter dtype={dtype} layout={layout}", flush=True)
+    b = workloads.build_batch([37, 5, 64, 17], [3, 5, 2, 1], n_q=8, n_kv=2, head_dim=64, block_size=16,
+                              dtype=dtype, device="cpu", seed=3, num_blocks=24)
+    kv_host = b.kv_cache.clone()
+    _to(b, device)
+    if layout == "flat":
+        k, v = b.k_new, b.v_new
+    else:  # [B, n_kv, T, D] needs equal query lengths: use 4 x 2 tokens of the packed stream
+        k = b.k_new[:8].view(4, 2, 2, 64).transpose(1, 2)
+        v = b.v_new[:8].view(4, 2, 2, 64).transpose(1, 2)
+    n = k.shape[0] * (k.shape[2] if k.ndim == 4 else 1)
+    slots = b.slot_mapping[:n].clone()
+    reshape_and_cache(k, v, b.kv_cache, slots, 0, b.block_size)
+    torch.cuda.synchronize()
+    ref = kv_host.numpy() if dtype == torch.float32 else kv_host.view(torch.int16).numpy()
+    kk = k.cpu().numpy() if dtype == torch.float32 else k.cpu().contiguous().view(torch.int16).numpy()
+    vv = v.cpu().numpy() if dtype == torch.float32 else v.cpu().contiguous().view(torch.int16).numpy()
+    ora.reshape_and_cache(kk, vv, ref, slots.cpu().numpy(), 0, b.block_size)
+    got = b.kv_cache.cpu().numpy() if dtype == torch.float32 else bits(b.kv_cache)
+    assert np.array_equal(got, ref)
+
+
+def test_scatter_skips_negative_and_out_of_pool_slots(device):
+    kv = torch.zeros((2, 2, 4, 8, 2, 64), dtype=torch.bfloat16, device=device)
+    k = torch.randn(4, 2, 64, device=device).to(torch.bfloat16)
+    v = torch.randn(4, 2, 64, device=device).to(torch.bfloat16)
+    slots = torch.tensor([-1, 3, 4 * 8, 31], dtype=torch.int64, device=device)
+    reshape_and_cache(k, v, kv, slots, 1, 8)
+    torch.cuda.synchronize()
+    ref = torch.zeros_like(kv)
+    ref[1, 0, 0, 3], ref[1, 1, 0, 3] = k[1], v[1]
+    ref[1, 0, 3, 7], ref[1, 1, 3, 7] = k[3], v[3]
+    assert torch.equal(kv, ref)
+
+
+def test_scatter_full_decode_step(device):
+    """C2 shape: the 256 new tokens land in their slots; nothing else changes."""
+    b = workloads.llama_decode(device=device, seed=1)
+    before = b.kv_cache.clone()
+    reshape_and_cache(b.k_new, b.v_new, b.kv_cache, b.slot_mapping, 0, 16)
+    torch.cuda.synchronize()
+    s = b.slot_mapping
+    blk, off = s // 16, s % 16
+    assert torch.equal(b.kv_cache[0, 0, blk, off], b.k_new)
+    assert torch.equal(b.kv_cache[0, 1, blk, off], b.v_new)
+    b.kv_cache[0, 0, blk, off] = before[0, 0, blk, off]
+    b.kv_cache[0, 1, blk, off] = before[0, 1, blk, off]
+    assert torch.equal(b.kv_cache, before)
+
+
+# ---------------------------------------------------------------- decode
+
+
+def test_decode_qwen05_config(device):
+    """C1: fp16, 14/2 heads, D 64, 8 sequences, pool 512 blocks; scatter then decode."""
+    b = workloads.qwen05_decode(device="cpu", seed=0)
+    kv_host = b.kv_cache.clone()
+    _to(b, device)
+    reshape_and_cache(b.k_new, b.v_new, b.kv_cache, b.slot_mapping, 0, 16)
+    out = paged_attention_decode(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
+    assert out.shape == (8, 1, 14, 64) and out.dtype == torch.float16
+    kv = kv_host.float().numpy().astype(np.float64)
+    kk, vv = f64(b.k_new), f64(b.v_new)
+    ora.reshape_and_cache(kk, vv, kv, b.slot_mapping.cpu().numpy(), 0, 16)
+    ref = ora.paged_attention(f64(b.padded_q()), kv, tables_array(b.tables_host, b.block_tables.shape[1]),
+                              np.array(b.ctx_host), 0, b.scale, 16)
+    assert_attn_close(out, ref, "qwen05 decode")
+
+
+EDGE_LENS = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 100, 257, 1000, 2049, 4000]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("block_size", [8, 16, 32])
+def test_decode_llama_shape_edge_lengths(device, dtype, block_size):
+    print(f"decode llama-shape dtype={dtype} bs={block_size}", flush=True)
+    b = workloads.build_batch(EDGE_LENS, [1] * len(EDGE_LENS), n_q=32, n_kv=8, head_dim=128,
+                              block_size=block_size, dtype=dtype, device="cpu", seed=11)
+    ref = _oracle_padded(b)
+    _to(b, device)
+    out = paged_attention_decode(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale,
+                                 block_size)
+    assert_attn_close(out, ref, f"decode bs={block_size}")
+
+
+@pytest.mark.parametrize("n_q,n_kv,tq", [(32, 8, 2), (32, 8, 4), (16, 8, 8), (14, 2, 2), (8, 8, 16)])
+def test_decode_multi_query_rows_causal(device, n_q, n_kv, tq):
+    """Tq > 1 through the decode tile (n_rep * Tq <= 16 rows): causal offsets per row."""
+    lens = [tq, tq + 1, 40, 333, 1024]
+    b = workloads.build_batch(lens, [tq] * len(lens), n_q=n_q, n_kv=n_kv, head_dim=128, block_size=16,
+                              dtype=torch.bfloat16, device="cpu", seed=5)
+    ref = _oracle_padded(b)
+    _to(b, device)
+    out = paged_attention_decode(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
+    assert_attn_close(out, ref, f"decode tq={tq}")
+
+
+def test_decode_table_holes_and_zero_lengths(device):
+    """Negative / out-of-pool table entries are masked; empty sequences give zeros."""
+    b = workloads.build_batch([200, 64, 50, 0, 300], [1] * 5, n_q=32, n_kv=8, head_dim=128, block_size=16,
+                              dtype=torch.bfloat16, device="cpu", seed=9, num_blocks=64)
+    tables = [list(t) for t in b.tables_host]
+    tables[0][3] = -1
+    tables[2][1] = 10_000  # past the pool
+    tables[4][0] = -7
+    width = b.block_tables.shape[1]
+    bt = torch.full((5, width), -1, dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, : len(t)] = torch.tensor(t, dtype=torch.int32)
+    b.block_tables = bt
+    b.context_lens = torch.tensor([200, 64, 50, 0, 300], dtype=torch.int32)
+    ref = ora.paged_attention(f64(b.padded_q()), f64(b.kv_cache), tables_array(tables, width),
+                              np.array([200, 64, 50, 0, 300]), 0, b.scale, 16)
+    _to(b, device)
+    out = paged_attention_decode(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
+    assert_attn_close(out, ref, "holes")
+    assert torch.count_nonzero(out[3]) == 0
+
+
+def test_decode_head_dim_64_and_256(device):
+    for d in (64, 256):
+        b = workloads.build_batch([5, 77, 600], [1, 1, 1], n_q=16, n_kv=4, head_dim=d, block_size=16,
+                                  dtype=torch.bfloat16, device="cpu", seed=d)
+        ref = _oracle_padded(b)
+        _to(b, device)
+        out = paged_attention_decode(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0,
+                                     b.scale, 16)
+        assert_attn_close(out, ref, f"D={d}")
+
+
+def test_decode_full_llama_config_subset_checked(device):
+    """C2 at full size (256 sequences, lognormal lengths, 1.2x pool): the scatter of the
+    256 new tokens then split-K decode; 24 sequences (longest, shortest, random) checked."""
+    b = workloads.llama_decode(device=device, seed=0)
+    reshape_and_cache(b.k_new, b.v_new, b.kv_cache, b.slot_mapping, 0, 16)
+    out = paged_attention_decode(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
+    torch.cuda.synchronize()
+    ctx = np.array(b.ctx_host)
+    pick = sorted(set(np.argsort(ctx)[-8:].tolist() + np.argsort(ctx)[:8].tolist()
+                      + np.random.default_rng(0).choice(256, 8, replace=False).tolist()))
+    sub_tables = [b.tables_host[i] for i in pick]
+    pool, tables = gather_pool_f64(b.kv_cache, sub_tables)
+    q = f64(b.padded_q()[pick])
+    ref = ora.paged_attention(q, pool, tables_array(tables, max(len(t) for t in tables)), ctx[pick], 0,
+                              b.scale, 16)
+    assert_attn_close(out[pick], ref, "C2 subset")
+
+
+def test_decode_is_invariant_to_block_permutation(device):
+    """Relabelling physical blocks (and the tables with them) leaves outputs bit-identical."""
+    b = workloads.build_batch([700, 33, 1500], [1, 1, 1], n_q=32, n_kv=8, head_dim=128, block_size=16,
+                              dtype=torch.bfloat16, device=device, seed=21)
+    out1 = paged_attention_decode(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
+    nb = b.kv_cache.shape[2]
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(1)).to(device)
+    kv2 = torch.empty_like(b.kv_cache)
+    kv2[:, :, perm] = b.kv_cache
+    bt = b.block_tables.long()
+    bt2 = torch.where(bt >= 0, perm[bt.clamp_min(0)], bt).to(torch.int32)
+    out2 = paged_attention_decode(b.padded_q(), kv2, bt2, b.context_lens, 0, b.scale, 16)
+    assert torch.equal(out1, out2)
+
+
+def test_decode_shared_prefix_equals_private_copies(device):
+    """Prefix config (C4 shape, reduced batch): tables sharing 128 blocks == private copies."""
+    b = workloads.prefix_share(device=device, seed=2, batch=16)
+    out_shared = paged_attention_decode(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0,
+                                        b.scale, 16)
+    # give every sequence a private copy of the prefix blocks
+    nb = b.kv_cache.shape[2]
+    shared = b.tables_host[0][: b.shared_blocks]
+    extra = torch.cat([b.kv_cache[:, :, shared]] * b.batch, dim=2)
+    kv2 = torch.cat([b.kv_cache, extra], dim=2)
+    tables = []
+    for i, t in enumerate(b.tables_host):
+        fresh = list(range(nb + i * b.shared_blocks, nb + (i + 1) * b.shared_blocks))
+        tables.append(fresh + t[b.shared_blocks :])
+    bt2 = torch.tensor(tables_array(tables, b.block_tables.shape[1]), dtype=torch.int32, device=device)
+    out_private = paged_attention_decode(b.padded_q(), kv2, bt2, b.context_lens, 0, b.scale, 16)
+    assert torch.equal(out_shared, out_private)
+
+
+# ---------------------------------------------------------------- prefill
+
+
+@pytest.mark.parametrize("n_q,n_kv,tq,lens", [
+    (32, 8, 8, [8, 9, 100, 700]),
+    (32, 8, 33, [33, 64, 517]),
+    (8, 8, 20, [20, 21, 300]),
+    (32, 1, 1, [1, 50, 900]),          # MQA: 32 rows per KV head go to the prefill tile
+    (28, 4, 64, [64, 1000]),
+])
+def test_prefill_padded(device, n_q, n_kv, tq, lens):
+    print(f"prefill n_q={n_q} n_kv={n_kv} tq={tq}", flush=True)
+    b = workloads.build_batch(lens, [tq] * len(lens), n_q=n_q, n_kv=n_kv, head_dim=128, block_size=16,
+                              dtype=torch.bfloat16, device="cpu", seed=tq)
+    ref = _oracle_padded(b)
+    _to(b, device)
+    out = paged_attention_prefill(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
+    assert_attn_close(out, ref, f"prefill tq={tq}")
+
+
+def test_prefill_fp16_head_dim_64(device):
+    b = workloads.build_batch([96, 500], [96, 96], n_q=14, n_kv=2, head_dim=64, block_size=16,
+                              dtype=torch.float16, device="cpu", seed=4)
+    ref = _oracle_padded(b)
+    _to(b, device)
+    out = paged_attention_prefill(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
+    assert_attn_close(out, ref, "prefill fp16 D64")
+
+
+# ---------------------------------------------------------------- packed varlen
+
+
+def _oracle_varlen(b: workloads.PagedBatch, kv: np.ndarray) -> np.ndarray:
+    return ora.paged_attention_varlen(f64(b.q), kv, tables_array(b.tables_host, b.block_tables.shape[1]),
+                                      f64(b.cu_seqlens).astype(np.int64), np.array(b.ctx_host), 0,
+                                      b.scale, b.block_size)
+
+
+def test_varlen_mixed_step_reduced(device):
+    """C3 structure at reduced size: 24 decodes + 3 chunks of 96 with prior context, one stream."""
+    ctx, ql = workloads.mixed_step_lengths(seed=7, n_prefill=3, chunk=96, n_decode=24)
+    ctx = [min(c, 1200) if q == 1 else c for c, q in zip(ctx, ql)]
+    b = workloads.build_batch(ctx, ql, n_q=32, n_kv=8, head_dim=128, block_size=16, dtype=torch.bfloat16,
+                              device="cpu", seed=7)
+    kv_host = b.kv_cache.clone()
+    _to(b, device)
+    reshape_and_cache(b.k_new, b.v_new, b.kv_cache, b.slot_mapping, 0, 16)
+    out = paged_attention_varlen(b.q, b.kv_cache, b.block_tables, b.cu_seqlens, b.context_lens, 0, b.scale,
+                                 16, b.max_query_len)
+    kv = kv_host.float().numpy().astype(np.float64)
+    ora.reshape_and_cache(f64(b.k_new), f64(b.v_new), kv, b.slot_mapping.cpu().numpy(), 0, 16)
+    assert_attn_close(out, _oracle_varlen(b, kv), "varlen mixed")
+
+
+def test_varlen_equals_padded_calls(device):
+    """Packed step == the per-sequence padded calls concatenated."""
+    ctx, ql = [300, 45, 700, 64], [1, 1, 64, 32]
+    b = workloads.build_batch(ctx, ql, n_q=32, n_kv=8, head_dim=128, block_size=16, dtype=torch.bfloat16,
+                              device=device, seed=8)
+    out = paged_attention_varlen(b.q, b.kv_cache, b.block_tables, b.cu_seqlens, b.context_lens, 0, b.scale,
+                                 16, b.max_query_len)
+    cu = [0, 1, 2, 66, 98]
+    for i in range(4):
+        qi = b.q[cu[i]:cu[i + 1]].unsqueeze(0).transpose(1, 2)
+        oi = paged_attention_prefill(qi, b.kv_cache, b.block_tables[i:i + 1], b.context_lens[i:i + 1], 0,
+                                     b.scale, 16)
+        # same kernels, but the split-K partition (hence fp32 summation order) differs
+        assert_attn_close(out[cu[i]:cu[i + 1]], f64(oi[0]), f"sequence {i}")
+
+
+def test_varlen_full_mixed_step_subset_checked(device):
+    """C3 at full size: 192 decodes + 4 x 512-token chunks, 2240 tokens; the scatter then
+    attention; all decode rows of 12 sequences and the last 24 tokens of every chunk checked."""
+    b = workloads.mixed_step(device=device, seed=0)
+    reshape_and_cache(b.k_new, b.v_new, b.kv_cache, b.slot_mapping, 0, 16)
+    out = paged_attention_varlen(b.q, b.kv_cache, b.block_tables, b.cu_seqlens, b.context_lens, 0, b.scale,
+                                 16, b.max_query_len)
+    torch.cuda.synchronize()
+    cu = b.cu_seqlens.cpu().tolist()
+    picks = list(range(0, 192, 16)) + list(range(192, 196))
+    pool, tables = gather_pool_f64(b.kv_cache, [b.tables_host[i] for i in picks])
+    for k, i in enumerate(picks):
+        s0, s1 = cu[i], cu[i + 1]
+        m = min(24, s1 - s0)
+        qb = f64(b.q[s1 - m:s1]).transpose(1, 0, 2)
+        kk, vv, valid = ora.gather_kv(pool, 0, np.array(tables[k]), b.ctx_host[i], 16)
+        ref = ora.attend(qb, kk, vv, valid, b.ctx_host[i], b.scale)
+        assert_attn_close(out[s1 - m:s1], ref, f"C3 seq {i}")
