@@ -1,0 +1,286 @@
+"""Pins of the numpy attention oracle (``oracle/paged_attention.py``) -- CPU only.
+
+The reference holds no golden vectors for this path (only seeded tests), so each
+oracle function is checked against something that does not re-evaluate its own
+formula:
+  * the reference's own round-trip test (tests/kernels/test_paged_attention.py:19-43)
+    and mask test (tests/correctness/test_cache_and_sampler.py:204-214), restated;
+  * torch's scaled_dot_product_attention (float64, explicit boolean mask, GQA by
+    expansion) -- a library routine for the dense case;
+  * a pure-Python scalar loop with ``math.exp`` on tiny inputs;
+  * closed forms (uniform scores -> mean of V, a dominant key -> its V row) and
+    invariants (block relabelling, shared prefix, split-K merge, packed == per-sequence);
+  * the hand-derived known answers in tests/golden/known_answers.json.
+Each check is chosen so that a plausible slip (swapped block/offset, wrong GQA
+head map, off-by-one in the causal offset, a dropped scale) fails it.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_attention as ora
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "known_answers.json"
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _paged_from_dense(k, v, block_size, rng, extra_blocks=3):
+    """Scatter dense [S, n_kv, D] K/V of one sequence into a pool through a random table."""
+    s, n_kv, d = k.shape
+    nb = -(-s // block_size)
+    pool_blocks = nb + extra_blocks
+    perm = rng.permutation(pool_blocks)
+    table = perm[:nb]
+    kv = rng.standard_normal((1, 2, pool_blocks, block_size, n_kv, d))  # garbage outside the sequence
+    slots = np.array([table[t // block_size] * block_size + t % block_size for t in range(s)])
+    ora.reshape_and_cache(k, v, kv, slots, 0, block_size)
+    return kv, table
+
+
+# ---------------------------------------------------------------- scatter / gather
+
+
+@pytest.mark.parametrize("block_size", [8, 16, 32])
+@pytest.mark.parametrize("seq_len", [1, 17, 64])
+def test_scatter_gather_roundtrip_exact(block_size, seq_len):
+    """Restates tests/kernels/test_paged_attention.py:19-43: scatter then gather is the identity."""
+    rng = _rng(seq_len * 100 + block_size)
+    n_kv, d = 2, 8
+    k = rng.standard_normal((seq_len, n_kv, d))
+    v = rng.standard_normal((seq_len, n_kv, d))
+    kv, table = _paged_from_dense(k, v, block_size, rng)
+    kg, vg, valid = ora.gather_kv(kv, 0, np.concatenate([table, [-1] * 4]), seq_len, block_size)
+    assert valid.all()
+    assert np.array_equal(kg, k) and np.array_equal(vg, v)
+
+
+def test_scatter_matches_flat_slot_indexing():
+    """The pool viewed as [L, 2, NB*bs, n_kv, D] is indexed by the slot itself (paged_cache.py:31-32)."""
+    rng = _rng(1)
+    nb, bs, n_kv, d = 7, 4, 3, 5
+    kv = np.zeros((2, 2, nb, bs, n_kv, d))
+    k = rng.standard_normal((9, n_kv, d))
+    v = rng.standard_normal((9, n_kv, d))
+    slots = rng.permutation(nb * bs)[:9]
+    ora.reshape_and_cache(k, v, kv, slots, 1, bs)
+    flat = kv.reshape(2, 2, nb * bs, n_kv, d)
+    assert np.array_equal(flat[1, 0, slots], k)
+    assert np.array_equal(flat[1, 1, slots], v)
+    assert not flat[0].any()  # other layer untouched
+    untouched = np.setdiff1d(np.arange(nb * bs), slots)
+    assert not flat[1, :, untouched].any()
+
+
+def test_scatter_bnhd_input_is_token_major_b_then_t():
+    """``[B, n_kv, T, D]`` is flattened as token n = b*T + t (_flatten_kv, attention_ref.py:8-18)."""
+    rng = _rng(2)
+    b, n_kv, t, d = 3, 2, 4, 6
+    k = rng.standard_normal((b, n_kv, t, d))
+    kv = np.zeros((1, 2, 8, 4, n_kv, d))
+    slots = np.arange(b * t)[::-1].copy()
+    ora.reshape_and_cache(k, k, kv, slots, 0, 4)
+    flat = kv.reshape(1, 2, 32, n_kv, d)
+    for bi in range(b):
+        for ti in range(t):
+            assert np.array_equal(flat[0, 0, slots[bi * t + ti]], k[bi, :, ti, :])
+
+
+def test_scatter_skips_negative_and_out_of_pool_slots_and_checks_length():
+    kv = np.zeros((1, 2, 2, 4, 1, 2))
+    k = np.ones((3, 1, 2))
+    ora.reshape_and_cache(k, k, kv, np.array([-1, 8, 5]), 0, 4)
+    assert kv.sum() == 2 * 2  # only slot 5 written, K and V
+    assert kv[0, 0, 1, 1].sum() == 2
+    with pytest.raises(ValueError):
+        ora.reshape_and_cache(k, k, kv, np.array([0, 1]), 0, 4)
+    with pytest.raises(ValueError):
+        ora.reshape_and_cache(k, k[:2], kv, np.array([0, 1, 2]), 0, 4)
+
+
+def test_gather_masks_holes_and_truncates_to_table():
+    kv = np.arange(1 * 2 * 4 * 2 * 1 * 1, dtype=np.float64).reshape(1, 2, 4, 2, 1, 1)
+    k, v, valid = ora.gather_kv(kv, 0, np.array([2, -1, 9, 0]), 7, 2)
+    assert k.shape == (7, 1, 1)
+    assert valid.tolist() == [True, True, False, False, False, False, True]
+    assert k[0, 0, 0] == kv[0, 0, 2, 0, 0, 0] and k[6, 0, 0] == kv[0, 0, 0, 0, 0, 0]
+    k2, _, valid2 = ora.gather_kv(kv, 0, np.array([1]), 7, 2)  # table shorter than ceil(7/2)
+    assert k2.shape[0] == 2 and valid2.all()
+
+
+# ---------------------------------------------------------------- attention
+
+
+def _sdpa(q, k, v, tq, seq_len, scale):
+    """torch SDPA in float64: q [n_q, Tq, D], k/v [S, n_kv, D] -> [Tq, n_q, D]."""
+    n_q = q.shape[0]
+    n_kv = k.shape[1]
+    kt = torch.from_numpy(k).permute(1, 0, 2).repeat_interleave(n_q // n_kv, dim=0)
+    vt = torch.from_numpy(v).permute(1, 0, 2).repeat_interleave(n_q // n_kv, dim=0)
+    qt = torch.from_numpy(q)
+    key = torch.arange(k.shape[0])
+    qabs = torch.arange(seq_len - tq, seq_len)
+    mask = key[None, :] <= qabs[:, None]
+    out = torch.nn.functional.scaled_dot_product_attention(qt[None], kt[None], vt[None], attn_mask=mask,
+                                                           scale=scale)
+    return out[0].permute(1, 0, 2).numpy()
+
+
+@pytest.mark.parametrize("n_q,n_kv,tq,seq_len,bs", [
+    (4, 2, 1, 32, 16), (4, 2, 8, 32, 16), (32, 8, 1, 100, 16), (14, 2, 5, 77, 8), (8, 1, 3, 40, 32),
+    (6, 6, 6, 6, 4),
+])
+def test_paged_attention_equals_torch_sdpa(n_q, n_kv, tq, seq_len, bs):
+    """Dense torch SDPA (library routine) on the un-paged K/V equals the paged oracle."""
+    rng = _rng(n_q * 1000 + seq_len)
+    d = 16
+    k = rng.standard_normal((seq_len, n_kv, d))
+    v = rng.standard_normal((seq_len, n_kv, d))
+    q = rng.standard_normal((1, n_q, tq, d))
+    kv, table = _paged_from_dense(k, v, bs, rng)
+    scale = d**-0.5
+    got = ora.paged_attention(q, kv, table[None], np.array([seq_len]), 0, scale, bs)
+    ref = _sdpa(q[0], k, v, tq, seq_len, scale)
+    np.testing.assert_allclose(got[0], ref, rtol=1e-12, atol=1e-12)
+
+
+def test_attend_equals_scalar_loop():
+    """Pure-Python loop with math.exp: GQA map h // n_rep and query j at seq_len - Tq + j."""
+    rng = _rng(5)
+    n_q, n_kv, tq, s, d = 4, 2, 3, 6, 3
+    q = rng.standard_normal((n_q, tq, d))
+    k = rng.standard_normal((s, n_kv, d))
+    v = rng.standard_normal((s, n_kv, d))
+    scale = 0.7
+    got = ora.attend(q, k, v, np.ones(s, bool), s, scale)
+    for h in range(n_q):
+        g = h // (n_q // n_kv)
+        for j in range(tq):
+            last = s - tq + j
+            sc = [scale * sum(q[h, j, x] * k[t, g, x] for x in range(d)) for t in range(last + 1)]
+            mx = max(sc)
+            w = [math.exp(c - mx) for c in sc]
+            tot = sum(w)
+            for x in range(d):
+                ref = sum(w[t] * v[t, g, x] for t in range(last + 1)) / tot
+                assert abs(got[j, h, x] - ref) < 1e-12
+
+
+def test_uniform_scores_average_values_and_dominant_key_selects_row():
+    """Closed forms: q = 0 gives the mean of visible V; a huge score picks that key's V."""
+    rng = _rng(6)
+    s, d = 20, 4
+    k = rng.standard_normal((s, 1, d))
+    v = rng.standard_normal((s, 1, d))
+    out = ora.attend(np.zeros((1, 2, d)), k, v, np.ones(s, bool), s, 1.0)
+    np.testing.assert_allclose(out[0, 0], v[: s - 1, 0].mean(axis=0), atol=1e-14)  # query s-2 sees 0..s-2
+    np.testing.assert_allclose(out[1, 0], v[:, 0].mean(axis=0), atol=1e-14)
+    kk = np.zeros((s, 1, d))
+    kk[7, 0, 0] = 1.0
+    q = np.zeros((1, 1, d))
+    q[0, 0, 0] = 1.0
+    out = ora.attend(q, kk, v, np.ones(s, bool), s, 1e4)
+    np.testing.assert_allclose(out[0, 0], v[7, 0], atol=1e-12)
+
+
+def test_decode_row_has_no_mask_and_empty_rows_are_zero():
+    """Tq=1 sees every key (packed_causal_mask decode case); a row with no visible key is 0."""
+    rng = _rng(7)
+    k = rng.standard_normal((9, 1, 4))
+    v = rng.standard_normal((9, 1, 4))
+    q = rng.standard_normal((1, 1, 4))
+    full = ora.attend(q, k, v, np.ones(9, bool), 9, 0.5)
+    sc = 0.5 * (k[:, 0] @ q[0, 0])
+    w = np.exp(sc - sc.max())
+    np.testing.assert_allclose(full[0, 0], (w / w.sum()) @ v[:, 0], atol=1e-14)
+    none = ora.attend(q, k, v, np.zeros(9, bool), 9, 0.5)
+    assert not none.any()
+    out = ora.paged_attention(q[None], np.zeros((1, 2, 2, 4, 1, 4)), np.array([[0, 1]]), np.array([0]), 0, 1.0, 4)
+    assert out.shape == (1, 1, 1, 4) and not out.any()
+
+
+def test_causal_mask_matches_reference_mask_test():
+    """tests/correctness/test_cache_and_sampler.py:204-214: prefill 4x4 lower-triangular, decode 1x5 open."""
+    # an indicator V exposes which keys each query row averages over (q = 0 -> uniform weights)
+    s, tq = 4, 4
+    v = np.eye(s)[:, None, :]
+    out = ora.attend(np.zeros((1, tq, s)), np.zeros((s, 1, s)), v, np.ones(s, bool), s, 1.0)
+    allowed = out[:, 0, :] > 0
+    assert allowed.tolist() == np.tril(np.ones((4, 4), bool)).tolist()
+    out = ora.attend(np.zeros((1, 1, 5)), np.zeros((5, 1, 5)), np.eye(5)[:, None, :], np.ones(5, bool), 5, 1.0)
+    assert (out[0, 0] > 0).all()
+
+
+def test_block_relabelling_invariance_and_shared_prefix():
+    rng = _rng(8)
+    bs, n_kv, d, s = 4, 2, 8, 23
+    k = rng.standard_normal((s, n_kv, d))
+    v = rng.standard_normal((s, n_kv, d))
+    q = rng.standard_normal((1, 4, 2, d))
+    kv, table = _paged_from_dense(k, v, bs, rng)
+    base = ora.paged_attention(q, kv, table[None], np.array([s]), 0, 0.3, bs)
+    perm = rng.permutation(kv.shape[2])
+    kv2 = np.empty_like(kv)
+    kv2[:, :, perm] = kv
+    again = ora.paged_attention(q, kv2, perm[table][None], np.array([s]), 0, 0.3, bs)
+    assert np.array_equal(base, again)
+    # two sequences sharing the first 3 blocks == each with private copies
+    nb = kv.shape[2]
+    t2 = np.concatenate([table[:3], [nb]])
+    kv3 = np.concatenate([kv, kv[:, :, table[3:4]]], axis=2)
+    shared = ora.paged_attention(np.concatenate([q, q]), kv3, np.stack([table[:4], t2]), np.array([14, 14]), 0,
+                                 0.3, bs)
+    assert np.array_equal(shared[0], shared[1])
+
+
+def test_split_k_merge_equals_single_pass():
+    rng = _rng(9)
+    q = rng.standard_normal((5, 16))
+    k = rng.standard_normal((70, 16))
+    v = rng.standard_normal((70, 16))
+    parts = [ora.partial_attention(q, k[a:b], v[a:b], 0.25) for a, b in [(0, 13), (13, 40), (40, 70)]]
+    merged = ora.merge_partials(parts)
+    single = ora.attend(q[:, None, :], k[:, None, :], v[:, None, :], np.ones(70, bool), 70, 0.25)[0]
+    # attend() treats the 5 rows as heads of one query token; shapes [5, 16] either way
+    np.testing.assert_allclose(merged, single, atol=1e-13)
+
+
+def test_varlen_equals_per_sequence_calls():
+    rng = _rng(10)
+    bs, n_q, n_kv, d = 8, 4, 2, 8
+    ctx = [5, 30, 17]
+    ql = [1, 6, 17]
+    pool = rng.standard_normal((1, 2, 20, bs, n_kv, d))
+    tables = np.full((3, 4), -1)
+    perm = rng.permutation(20)
+    c = 0
+    for i, n in enumerate(ctx):
+        nb = -(-n // bs)
+        tables[i, :nb] = perm[c : c + nb]
+        c += nb
+    cu = np.concatenate([[0], np.cumsum(ql)])
+    q = rng.standard_normal((cu[-1], n_q, d))
+    got = ora.paged_attention_varlen(q, pool, tables, cu, np.array(ctx), 0, 0.4, bs)
+    for i in range(3):
+        qi = q[cu[i] : cu[i + 1]].transpose(1, 0, 2)[None]
+        ref = ora.paged_attention(qi, pool, tables[i : i + 1], np.array([ctx[i]]), 0, 0.4, bs)
+        assert np.array_equal(got[cu[i] : cu[i + 1]], ref[0])
+
+
+def test_known_answers_attention():
+    """Hand-derived vectors (tests/golden/known_answers.json), no oracle involved in making them."""
+    gold = json.loads(GOLDEN.read_text())["attention"]
+    for case in gold:
+        kv = np.array(case["kv_cache"], dtype=np.float64)
+        out = ora.paged_attention(np.array(case["q"], dtype=np.float64), kv, np.array(case["block_tables"]),
+                                  np.array(case["seq_lens"]), 0, case["scale"], case["block_size"])
+        np.testing.assert_allclose(out, np.array(case["expected"]), atol=1e-12, err_msg=case["name"])
