@@ -42,6 +42,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the host-side reference timing")
     ap.add_argument("--skip-extra", action="store_true", help="headline only (no packed / prefix lines)")
+    ap.add_argument("--only", choices=["all", "w4a16"], default="all",
+                    help="w4a16: run the C5 section alone and print it (profiling aid)")
     return ap.parse_args()
 
 
@@ -62,6 +64,36 @@ def time_loop(fn, steps: int, warmup: int):
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
     return start.elapsed_time(end) / steps, wall
+
+
+def graph_time(fn, calls: int, replays: int, warmup: int = 3):
+    """Mean ms per call of ``fn`` with ``calls`` calls captured in one HIP graph and the
+    graph replayed ``replays`` times between HIP events: host dispatch cost (Python,
+    ctypes) is kept out of kernels that run for a few microseconds."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(warmup):  # first calls allocate the output pool and workspace
+            fn()
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(calls):
+            fn()
+    with torch.cuda.stream(s):
+        g.replay()
+        s.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(s)
+        for _ in range(replays):
+            g.replay()
+        end.record(s)
+    end.synchronize()
+    ms = start.elapsed_time(end) / (replays * calls)
+    del g
+    return ms
 
 
 def decode_bytes(b) -> dict:
@@ -146,6 +178,61 @@ def cpu_baseline(b, seed: int) -> dict:
     }
 
 
+C5_SHAPES = [(4096, 6144, "qkv"), (4096, 4096, "o"), (4096, 14336, "gate"), (4096, 14336, "up"),
+             (14336, 4096, "down")]
+ROTATE_BYTES = 640 << 20  # distinct weight bytes cycled per case: > 2x the 256 MB MALL
+
+
+def w4a16_section(dev, steps: int, warmup: int) -> dict:
+    """C5: W4A16 linears of one Llama-3-8B layer at M in {1, 16, 64, 256}.
+
+    Each case cycles through enough weight copies that the MALL cannot serve
+    them; bytes = the reference-format operands read once + activations + output.
+    The calls of one cycle are captured in a HIP graph (see ``graph_time``).
+    """
+    import torch
+
+    from slipstream_amd import workloads
+    from slipstream_amd.kernels import w4a16_gemm
+
+    cases = []
+    layer_us = {}
+    for k, n, name in C5_SHAPES:
+        if name == "up":  # same shape as gate: timed once, counted twice in the layer total
+            continue
+        base = workloads.w4a16_linear(k, n, 256, device=dev, seed=k + n)
+        copies = max(2, min(64, -(-ROTATE_BYTES // base.weight_bytes())))
+        qws = [base.qweight] + [base.qweight.clone() for _ in range(copies - 1)]
+        scs = [base.scales] + [base.scales.clone() for _ in range(copies - 1)]
+        qzs = [base.qzeros] + [base.qzeros.clone() for _ in range(copies - 1)]
+        for m in (1, 16, 64, 256):
+            x = base.x[:m].contiguous()
+            idx = [0]
+
+            def call():
+                i = idx[0] % copies
+                idx[0] += 1
+                return w4a16_gemm(x, qws[i], scs[i], qzs[i], base.group_size)
+
+            ms = graph_time(call, copies, max(3, steps // copies))
+            wbytes = n * k // 2 + n * (k // base.group_size) * (base.scales.element_size() + 4)
+            nbytes = wbytes + 2 * m * k + 2 * m * n
+            flops = 2.0 * m * n * k
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            tfl = flops / (ms * 1e-3) / 1e12
+            bound = "mfma" if flops / nbytes > 312 else "hbm"
+            frac = tfl / BF16_PEAK_TFLOPS if bound == "mfma" else gbs / HBM_PEAK_GBS
+            cases.append({"linear": name, "k": k, "n": n, "m": m, "us": round(ms * 1e3, 2), "GBps": round(gbs, 1),
+                          "TFLOPs": round(tfl, 2), "bound": bound, "frac": round(frac, 4),
+                          "weight_copies": copies})
+            layer_us[m] = layer_us.get(m, 0.0) + ms * 1e3 * (2 if name == "gate" else 1)
+        del qws, scs, qzs, base
+        torch.cuda.empty_cache()
+    return {"workload": "C5 W4A16 linears of one Llama-3-8B layer (qkv 4096x6144, o 4096x4096, gate/up "
+                        "4096x14336, down 14336x4096), g=128, fp16 scales, zeros 8, bf16 x",
+            "cases": cases, "layer_us_by_m": {str(m): round(v, 2) for m, v in layer_us.items()}}
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -173,6 +260,10 @@ def main() -> int:
     _ffi.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.only == "w4a16":  # profiling aid: the C5 section alone
+        print(json.dumps({"w4a16": w4a16_section(dev, args.steps, args.warmup)}), flush=True)
+        return 0
 
     # ---- C2: headline decode step ------------------------------------------------
     b = workloads.llama_decode(device=dev, seed=args.seed)
@@ -283,6 +374,9 @@ def main() -> int:
         }
         del p, pq
         torch.cuda.empty_cache()
+
+        # ---- C5: W4A16 linears ------------------------------------------------------
+        result["w4a16"] = w4a16_section(dev, args.steps, args.warmup)
 
     if not args.no_cpu_baseline:
         b = workloads.llama_decode(device=dev, seed=args.seed)

@@ -117,6 +117,38 @@ int ss_paged_attention_varlen(const void* q, void* out, const void* k_cache, con
                               int64_t bt_stride, float scale, int dtype, void* workspace,
                               int64_t workspace_bytes, void* stream);
 
+/*
+ * W4A16 linear: out[m, :] = x[m, :] @ dequant(W)^T, no bias.
+ * Replaces w4a16_gemm (slipstream/kernels/quant_gemm.py:23-42), whose body is
+ * w4a16_gemm_ref (slipstream/kernels/quant_ref.py:119-133); weight format of
+ * quant_ref.py:8-20,45-69,103-116:
+ *   qweight [n, k/8] int32, row-major: nibble j of word w of row o is q[o, 8w + j]
+ *           at bits 4j..4j+3 (two's-complement storage of the 32-bit pattern);
+ *   scales  [n, k/group_size], dtype scale_dtype (SS_DTYPE_F16/BF16/F32), row-major;
+ *   qzeros  [n, k/group_size] int32, row-major (values 0..15 as produced by
+ *           quantize_w4a16; any int32 is accepted);
+ *   w[o, c] = (q[o, c] - qzeros[o, c / group_size]) * scales[o, c / group_size].
+ * x [m, k] with row stride x_stride (elements, unit column stride), dtype
+ * act_dtype (SS_DTYPE_BF16/F16/F32); out [m, n] with row stride o_stride, same
+ * dtype as x. Accumulation is fp32 with the exact dequantised weight.
+ * group_size must be a positive multiple of 8 dividing k (else SS_ERR_INVALID,
+ * quant_ref.py:38-42). bf16/fp16 activations with k % 128 == 0 and
+ * group_size % 32 == 0 (16-byte aligned x rows and qweight, n*k/2 < 2^31, and
+ * a per-workgroup scale table of 16 * (2*k/group_size + 2) floats within 64 KiB
+ * of LDS: k/group_size <= 480 for m <= 16) take the MFMA kernel; everything
+ * else a scalar fp32 kernel. The result does not depend on timing (no
+ * cross-workgroup reduction).
+ * workspace: ss_w4a16_workspace_size() reports 0 bytes; the arguments are kept
+ * so a later kernel may use scratch without an ABI change (pass NULL, 0).
+ */
+int ss_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int group_size, int act_dtype,
+                            int64_t* bytes);
+
+int ss_w4a16_gemm(const void* x, void* out, const int32_t* qweight, const void* scales,
+                  const int32_t* qzeros, int64_t m, int64_t n, int64_t k, int group_size,
+                  int64_t x_stride, int64_t o_stride, int act_dtype, int scale_dtype,
+                  void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

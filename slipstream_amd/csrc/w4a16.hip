@@ -1,0 +1,554 @@
+// W4A16 linear y = x @ dequant(W)^T for gfx950 (group-wise asymmetric int4 weights,
+// 16-bit activations, fp32 accumulation).
+//
+// Format (slipstream/kernels/quant_ref.py:8-20,45-69,103-116): qweight [N, K/8]
+// int32, nibble n of word j of row o = q[o, 8j + n] at bits 4n; scales [N, K/g]
+// (fp16, bf16 or fp32); qzeros [N, K/g] int32; w = (q - zero) * scale.
+//
+// Fast path (bf16/fp16 activations, K % 128 == 0, g % 32 == 0): MFMA 16x16x32,
+// A = activation rows, B = weight rows dequantised in registers by the exponent
+// trick: a nibble q OR-ed into the mantissa of 2^7 (bf16) or 2^10 (fp16) is
+// exactly MAGIC + q, one v_and_or per pair of weights. For each quantisation
+// group the MFMA accumulates G = sum_k x (MAGIC + q), and a second MFMA against
+// an all-ones B gives X = sum_k x in the same accumulator layout; then
+//     sum_k x (q - z) s = s * G - s * (MAGIC + z) * X,
+// exact for any zero point. The nibble pairs come out in the order
+// (k0,k4),(k1,k5),(k2,k6),(k3,k7) of each word, and every activation fragment is
+// permuted the same way in registers (v_perm_b32), so the dot products pair up.
+//
+// Work split: a workgroup owns 16*NS weight rows and 16*MT activation rows; its
+// KW waves split K into contiguous slices (each wave streams its own slice of
+// the rows: coalesced 16-byte loads, the next block in flight while the current
+// one computes), and one LDS pass adds the slices in wave order. There is no
+// synchronisation between workgroups, so the result does not depend on timing.
+//
+// Generic path (any other shape, fp32 activations): one thread per output,
+// fp32 dequant and dot product.
+#include "ss_common.h"
+
+namespace ss {
+namespace {
+
+struct W4Params {
+  const void* x;
+  void* out;
+  const uint32_t* qw;
+  const void* sc;
+  const int32_t* qz;
+  int64_t x_stride, o_stride;  // elements
+  int m, n, k, g, groups, sdt;
+  int kw;  // waves (K slices) per workgroup
+};
+
+constexpr int kMaxKW = 8;
+
+template <typename T>
+struct W4Elem;
+template <>
+struct W4Elem<bf16_t> {
+  static constexpr uint32_t kMagicPair = 0x43004300u;  // bf16 128.0 in both halves
+  static constexpr uint32_t kOnePair = 0x3F803F80u;    // bf16 1.0 in both halves
+  static constexpr float kMagic = 128.f;
+  static __device__ __forceinline__ float to_f32(uint32_t h) { return __builtin_bit_cast(float, h << 16); }
+};
+template <>
+struct W4Elem<f16_t> {
+  static constexpr uint32_t kMagicPair = 0x64006400u;  // fp16 1024.0 in both halves
+  static constexpr uint32_t kOnePair = 0x3C003C00u;    // fp16 1.0 in both halves
+  static constexpr float kMagic = 1024.f;
+  static __device__ __forceinline__ float to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(f16_t, (uint16_t)h);
+  }
+};
+
+__device__ __forceinline__ float load_scale(const void* s, int64_t i, int sdt) {
+  if (sdt == SS_DTYPE_F16) return (float)((const f16_t*)s)[i];
+  if (sdt == SS_DTYPE_BF16) return __builtin_bit_cast(float, (uint32_t)((const uint16_t*)s)[i] << 16);
+  return ((const float*)s)[i];
+}
+
+// A constant held in a VGPR. gfx9 VOP3 instructions take no literal and read at most
+// one SGPR, so (w & mask) | magic becomes one v_and_or_b32 only when the magic word
+// already sits in a VGPR (the mask goes to the SGPR slot); otherwise it takes a
+// v_and and a v_or with literals.
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t c) {
+  uint32_t v;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(v) : "s"(c));
+  return v;
+}
+
+// Eight nibbles -> eight 16-bit (MAGIC + q) values in the order k0,k4,k1,k5,k2,k6,k3,k7.
+__device__ __forceinline__ u32x4 nibbles_to_operand(uint32_t w, uint32_t magic) {
+  return u32x4{(w & 0x000F000Fu) | magic, ((w >> 4) & 0x000F000Fu) | magic, ((w >> 8) & 0x000F000Fu) | magic,
+               ((w >> 12) & 0x000F000Fu) | magic};
+}
+
+// Eight consecutive 16-bit x values -> the same order as nibbles_to_operand.
+__device__ __forceinline__ u32x4 permute_x(u32x4 d) {
+  return u32x4{pick_halves<0, 0>(d[0], d[2]), pick_halves<1, 1>(d[0], d[2]), pick_halves<0, 0>(d[1], d[3]),
+               pick_halves<1, 1>(d[1], d[3])};
+}
+
+// Raw buffer resource over [base, base + bytes): loads past the end return 0, and a
+// per-iteration offset rides in the scalar offset, so the loop does no 64-bit
+// address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// MT: 16-row activation tiles; NS: 16-row weight tiles; BIT: 128-key iterations
+// per pipeline block; WIDE: g % 128 == 0 (one group per iteration, a lane holds 32
+// consecutive keys of its row: one 16-byte load), else g % 32 == 0 (one group per
+// 32-key MFMA step, 4-byte loads); XLDS: the workgroup's activation rows (all of K,
+// permuted) and their per-fold sums are staged in LDS once -- used when they fit;
+// otherwise every wave loads its own activation fragments and sums them with an
+// all-ones MFMA.
+//
+// Dynamic LDS: [XLDS: x rows (K + 8 elements each) | fold sums [K/UNIT][16*MT]]
+//              [scale table: 16*NS rows x (2*groups + 2) floats, pairs (s, s*(MAGIC+z))]
+// and, once every wave is past the main loop, the same bytes again as the
+// reduction buffer (kw - 1) x MT*NS x 64 x f32x4.
+template <typename T, int MT, int NS, int BIT, bool WIDE, bool XLDS>
+__global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
+  constexpr int SPI = WIDE ? 1 : 4;      // quantisation groups (folds) per 128-key iteration
+  constexpr int UNIT = WIDE ? 128 : 32;  // keys per fold
+  typedef W4Elem<T> E;
+  extern __shared__ __attribute__((aligned(16))) char s_dyn[];
+
+  const int lane = threadIdx.x & 63;
+  // wave-uniform by construction; readfirstlane lets the compiler keep everything
+  // derived from it (slice bounds, buffer offsets) in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ln = lane & 15, kg = lane >> 4;
+  const int n0 = blockIdx.x * 16 * NS;
+  const int m0 = blockIdx.y * 16 * MT;
+  const int rows = min(16 * MT, p.m - m0);
+  const int iters = p.k >> 7;
+  const int per = (iters + p.kw - 1) / p.kw;
+  const int it0 = wave * per;
+  const int it1 = min(iters, it0 + per);
+  const int lrow = p.k + 8;           // LDS row of x, elements (16-byte skew per row)
+  const int szrow = 2 * p.groups + 2;  // LDS row of the scale table, floats (8-byte skew per row)
+  const uint32_t magic = in_vgpr(E::kMagicPair);
+
+  T* s_x = (T*)s_dyn;
+  const size_t x_bytes = XLDS ? (size_t)rows * lrow * sizeof(T) + (size_t)(p.k / UNIT) * 16 * MT * 4 : 0;
+  float* s_xs = (float*)(s_dyn + (XLDS ? (size_t)rows * lrow * sizeof(T) : 0));
+  float* s_sz = (float*)(s_dyn + x_bytes);
+  f32x4* s_red = (f32x4*)s_dyn;  // aliases the tables above, used after a barrier
+
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(p.qw, (uint32_t)((int64_t)p.n * p.k / 2));
+  int w_off[NS];  // byte offset of this lane's part of its weight row
+#pragma unroll
+  for (int ns = 0; ns < NS; ++ns) {
+    const int r = min(n0 + ns * 16 + ln, p.n - 1);  // rows past N repeat row N-1; never stored
+    w_off[ns] = r * (p.k / 2) + (WIDE ? 16 * kg : 4 * kg);
+  }
+
+  struct WBlock {
+    u32x4 w[NS][BIT];
+  };
+  struct XBlock {
+    u32x4 x[XLDS ? 1 : MT][XLDS ? 1 : BIT][4];
+  };
+
+  // Weight loads only (no use), always in range: iterations past the slice reload
+  // the slice's last iteration and fold with scale 0.
+  auto load_w = [&](int itb, WBlock& wb) {
+#pragma unroll
+    for (int it = 0; it < BIT; ++it) {
+      const int kk = min(itb + it, it1 - 1) << 7;
+#pragma unroll
+      for (int ns = 0; ns < NS; ++ns) {
+        if (WIDE) {
+          wb.w[ns][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, w_off[ns], kk / 2, 0));
+        } else {
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            wb.w[ns][it][s] = __builtin_amdgcn_raw_buffer_load_b32(rw, w_off[ns], kk / 2 + 16 * s, 0);
+        }
+      }
+    }
+  };
+
+  // The first block's weights go out before the prologue so their latency overlaps it.
+  WBlock wa, wb;
+  if (it0 < it1) load_w(it0, wa);
+
+  // ---- prologue: scale table (+ activations) into LDS
+  for (int q = threadIdx.x; q < 16 * NS * p.groups; q += blockDim.x) {
+    const int r = q / p.groups, gi = q - r * p.groups;
+    const int64_t si = (int64_t)min(n0 + r, p.n - 1) * p.groups + gi;
+    const float sc = load_scale(p.sc, si, p.sdt);
+    s_sz[r * szrow + 2 * gi] = sc;
+    s_sz[r * szrow + 2 * gi + 1] = sc * (E::kMagic + (float)p.qz[si]);  // s * (MAGIC + z)
+  }
+  if (XLDS) {
+    // rows [m0, m0 + rows) of x for all of K, permuted, plus their fold sums
+    constexpr int GL = UNIT / 8;  // staging lanes per fold (consecutive lanes)
+    const int cols = p.k / 8;
+    for (int q = threadIdx.x; q < rows * cols; q += blockDim.x) {
+      const int r = q / cols, c = q - r * cols;
+      const u32x4 v = load16((const T*)p.x + (int64_t)(m0 + r) * p.x_stride + 8 * c);
+      store16(&s_x[r * lrow + 8 * c], permute_x(v));
+      float sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sum += E::to_f32(v[j] & 0xFFFFu) + E::to_f32(v[j] >> 16);
+#pragma unroll
+      for (int o = 1; o < GL; o <<= 1) sum += __shfl_xor(sum, o);
+      if (c % GL == 0) s_xs[(c / GL) * 16 * MT + r] = sum;
+    }
+    // sums of rows past M are 0 (their outputs are never stored)
+    for (int q = threadIdx.x; q < (p.k / UNIT) * 16 * MT; q += blockDim.x)
+      if (q % (16 * MT) >= rows) s_xs[q] = 0.f;
+  }
+  __syncthreads();
+
+  // Activation rows past M read row M-1 (a valid address); they only feed output
+  // rows past M, which are never stored (each MFMA output row depends on its own
+  // input row alone).
+  const T* xrow[MT];
+  int xl[MT];  // LDS row (XLDS)
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    xrow[mt] = (const T*)p.x + (int64_t)min(m0 + mt * 16 + ln, p.m - 1) * p.x_stride;
+    xl[mt] = min(mt * 16 + ln, rows - 1) * lrow;
+  }
+
+  f32x4 acc[MT][NS];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) acc[mt][ns] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto load_x = [&](int itb, XBlock& xb) {
+    if (XLDS) return;
+#pragma unroll
+    for (int it = 0; it < BIT; ++it) {
+      const int kk = min(itb + it, it1 - 1) << 7;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int koff = kk + (WIDE ? 32 * kg + 8 * s : 32 * s + 8 * kg);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) xb.x[XLDS ? 0 : mt][XLDS ? 0 : it][s] = load16(xrow[mt] + koff);
+      }
+    }
+  };
+
+  const u32x4 ones = {E::kOnePair, E::kOnePair, E::kOnePair, E::kOnePair};
+  auto compute = [&](int itb, const WBlock& wblk, const XBlock& xb) {
+#pragma unroll
+    for (int it = 0; it < BIT; ++it) {
+      // no branch: an iteration past the slice computes on reloaded data and folds
+      // with scale 0 (a branch here lets the compiler sink this block's loads into it)
+      const bool live = itb + it < it1;
+      const int kk = min(itb + it, it1 - 1) << 7;
+      f32x4 G[MT][NS], X[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        X[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ns = 0; ns < NS; ++ns) G[mt][ns] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        u32x4 a[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          if (XLDS) {
+            a[mt] = load16(&s_x[xl[mt] + kk + (WIDE ? 32 * kg + 8 * s : 32 * s + 8 * kg)]);
+          } else {
+            a[mt] = permute_x(xb.x[XLDS ? 0 : mt][XLDS ? 0 : it][s]);
+            X[mt] = Elem<T>::mfma(a[mt], ones, X[mt]);
+          }
+        }
+#pragma unroll
+        for (int ns = 0; ns < NS; ++ns) {
+          const u32x4 b = nibbles_to_operand(wblk.w[ns][it][s], magic);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) G[mt][ns] = Elem<T>::mfma(a[mt], b, G[mt][ns]);
+        }
+        if (!WIDE || s == 3) {  // end of a fold unit: fold it into acc
+          const int kf = kk + (WIDE ? 0 : 32 * s);
+          if (XLDS) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              X[mt] = *reinterpret_cast<const f32x4*>(&s_xs[(kf / UNIT) * 16 * MT + mt * 16 + 4 * kg]);
+          }
+          const int gi = kf / p.g;
+#pragma unroll
+          for (int ns = 0; ns < NS; ++ns) {
+            const float2 sz = *reinterpret_cast<const float2*>(&s_sz[(ns * 16 + ln) * szrow + 2 * gi]);
+            const float sc = live ? sz.x : 0.f;
+            const float cz = live ? sz.y : 0.f;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[mt][ns][e] = fmaf(sc, G[mt][ns][e], fmaf(-cz, X[mt][e], acc[mt][ns][e]));
+              G[mt][ns] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) X[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
+  };
+
+  if (it0 < it1) {
+    // Issue order: weights(b), then x(b), then weights(b+1); compute(b) waits for x(b)
+    // and so for everything issued before it, never for weights(b+1). The prefetch is
+    // unconditional (past the slice it reloads the slice's last iteration) so every
+    // path through the loop has the same loads in flight and the waits stay exact.
+    // sched_barrier(0): the scheduler keeps each block's loads issued together ahead of
+    // its compute instead of spreading them between the MFMAs.
+    XBlock xs;
+    int itb = it0;
+    while (true) {
+      load_x(itb, xs);
+      load_w(itb + BIT, wb);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(itb, wa, xs);
+      __builtin_amdgcn_sched_barrier(0);
+      itb += BIT;
+      if (itb >= it1) break;
+      load_x(itb, xs);
+      load_w(itb + BIT, wa);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(itb, wb, xs);
+      __builtin_amdgcn_sched_barrier(0);
+      itb += BIT;
+      if (itb >= it1) break;
+    }
+  }
+
+  // ---- K slices -> one sum, in wave order
+  __syncthreads();  // all waves are done with the tables the reduction buffer overlays
+  if (wave > 0) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int ns = 0; ns < NS; ++ns) s_red[((wave - 1) * MT * NS + mt * NS + ns) * 64 + lane] = acc[mt][ns];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  for (int w = 1; w < p.kw; ++w) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int ns = 0; ns < NS; ++ns) acc[mt][ns] += s_red[((w - 1) * MT * NS + mt * NS + ns) * 64 + lane];
+  }
+  // lane holds C[m0 + mt*16 + 4kg + e][n0 + ns*16 + ln]
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) {
+      const int n = n0 + ns * 16 + ln;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + mt * 16 + 4 * kg + e;
+        if (m < p.m && n < p.n) ((T*)p.out)[(int64_t)m * p.o_stride + n] = (T)acc[mt][ns][e];
+      }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ float elem_to_f32(T v) {
+  return (float)v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void w4a16_generic_kernel(const W4Params p) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)p.m * p.n) return;
+  const int m = (int)(idx / p.n), n = (int)(idx - (int64_t)m * p.n);
+  const T* xr = (const T*)p.x + (int64_t)m * p.x_stride;
+  const uint32_t* wr = p.qw + (int64_t)n * (p.k >> 3);
+  float acc = 0.f;
+  for (int j = 0; j < (p.k >> 3); ++j) {
+    const uint32_t w = wr[j];
+    const int gi = (8 * j) / p.g;
+    const int64_t si = (int64_t)n * p.groups + gi;
+    const float s = load_scale(p.sc, si, p.sdt);
+    const float z = (float)p.qz[si];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc = fmaf(elem_to_f32(xr[8 * j + i]), ((float)((w >> (4 * i)) & 15u) - z) * s, acc);
+  }
+  ((T*)p.out)[(int64_t)m * p.o_stride + n] = (T)acc;
+}
+
+// ---- host side -------------------------------------------------------------
+
+struct W4Plan {
+  bool fast;
+  bool wide;
+  bool xlds;
+  int mt, ns, bit, kw;
+  int m_blocks, n_tiles;
+  size_t lds;
+};
+
+constexpr size_t kLdsBudget = 64 * 1024;  // LDS bytes per workgroup
+
+W4Plan plan_w4a16(int64_t m, int64_t n, int64_t k, int g, bool act16) {
+  W4Plan pl = {};
+  pl.fast = act16 && k % 128 == 0 && g % 32 == 0 && k > 0 && n * k / 2 < ((int64_t)1 << 31);
+  pl.wide = g % 128 == 0;
+  if (!pl.fast) return pl;
+  const size_t unit = pl.wide ? 128 : 32;
+  const int64_t groups = k / g;
+  const int iters = (int)(k / 128);
+  const int64_t want = 8LL * ss_host::device_cu_count();  // waves in flight to cover HBM latency
+  // x staged in LDS when one 16-row tile of it fits beside the scale table
+  const int64_t rows1 = m < 16 ? m : 16;
+  const size_t x1 = (size_t)rows1 * (k + 8) * 2 + (size_t)(k / unit) * 16 * 4;
+  const size_t sz1 = (size_t)16 * (2 * groups + 2) * 4;
+  if (m <= 16 && x1 + sz1 <= kLdsBudget) {
+    pl.mt = 1, pl.ns = 1, pl.bit = 4, pl.xlds = true;
+  } else if (m <= 16) {
+    pl.mt = 1, pl.ns = 4, pl.bit = 2;  // 64 weight rows share each activation fragment
+  } else if (m <= 32) {
+    pl.mt = 2, pl.ns = 2, pl.bit = 2;
+  } else {
+    pl.mt = 4, pl.ns = 2, pl.bit = 1;
+  }
+  pl.m_blocks = (int)((m + 16 * pl.mt - 1) / (16 * pl.mt));
+  pl.n_tiles = (int)((n + 16 * pl.ns - 1) / (16 * pl.ns));
+  // K slices per workgroup, with at least two 128-key iterations per slice
+  const int64_t wgs = (int64_t)pl.m_blocks * pl.n_tiles;
+  pl.kw = wgs * 4 >= want ? 4 : kMaxKW;
+  while (pl.kw > 1 && iters < 2 * pl.kw) pl.kw >>= 1;
+  const size_t red = (size_t)(pl.kw - 1) * pl.mt * pl.ns * 64 * 16;
+  const size_t xb = pl.xlds ? x1 : 0;
+  const size_t szb = (size_t)16 * pl.ns * (2 * groups + 2) * 4;
+  pl.lds = xb + szb > red ? xb + szb : red;  // the reduction reuses the tables' bytes
+  if (pl.lds > kLdsBudget) pl.fast = false;  // scale table too large: scalar kernel
+  return pl;
+}
+
+template <typename T, int MT, int NS, int BIT, bool X>
+int launch_w4a16_x(const W4Params& p, const W4Plan& pl, hipStream_t stream) {
+  dim3 grid((unsigned)pl.n_tiles, (unsigned)pl.m_blocks);
+  dim3 block(64 * pl.kw);
+  if (pl.wide)
+    hipLaunchKernelGGL((w4a16_kernel<T, MT, NS, BIT, true, X>), grid, block, pl.lds, stream, p);
+  else
+    hipLaunchKernelGGL((w4a16_kernel<T, MT, NS, BIT, false, X>), grid, block, pl.lds, stream, p);
+  return ss_host::launch_status("w4a16 gemm");
+}
+
+template <typename T>
+int launch_w4a16_typed(const W4Params& p, const W4Plan& pl, hipStream_t stream) {
+  if (pl.xlds) return launch_w4a16_x<T, 1, 1, 4, true>(p, pl, stream);
+  if (pl.mt == 1) return launch_w4a16_x<T, 1, 4, 2, false>(p, pl, stream);
+  if (pl.mt == 2) return launch_w4a16_x<T, 2, 2, 2, false>(p, pl, stream);
+  return launch_w4a16_x<T, 4, 2, 1, false>(p, pl, stream);
+}
+
+}  // namespace
+}  // namespace ss
+
+namespace {
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int check_w4a16(const char* who, int64_t m, int64_t n, int64_t k, int g, int act_dtype, int scale_dtype) {
+  if (m < 0 || n < 0 || k < 0) {
+    ss_host::set_error("%s: negative extent (m=%lld n=%lld k=%lld)", who, (long long)m, (long long)n, (long long)k);
+    return SS_ERR_INVALID;
+  }
+  if (g <= 0 || g % 8 != 0) {
+    ss_host::set_error("%s: group_size must be a positive multiple of 8, got %d", who, g);
+    return SS_ERR_INVALID;
+  }
+  if (k % g != 0) {
+    ss_host::set_error("%s: in_features %lld not divisible by group_size %d", who, (long long)k, g);
+    return SS_ERR_INVALID;
+  }
+  if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff || m * n > ((int64_t)1 << 40)) {
+    ss_host::set_error("%s: extents too large", who);
+    return SS_ERR_UNSUPPORTED;
+  }
+  if (act_dtype != SS_DTYPE_BF16 && act_dtype != SS_DTYPE_F16 && act_dtype != SS_DTYPE_F32) {
+    ss_host::set_error("%s: activation dtype code %d not supported", who, act_dtype);
+    return SS_ERR_UNSUPPORTED;
+  }
+  if (scale_dtype != SS_DTYPE_BF16 && scale_dtype != SS_DTYPE_F16 && scale_dtype != SS_DTYPE_F32) {
+    ss_host::set_error("%s: scale dtype code %d not supported", who, scale_dtype);
+    return SS_ERR_UNSUPPORTED;
+  }
+  return SS_OK;
+}
+}  // namespace
+
+extern "C" int ss_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int group_size, int act_dtype,
+                                       int64_t* bytes) {
+  int st = check_w4a16("w4a16 workspace", m, n, k, group_size, act_dtype, SS_DTYPE_F16);
+  if (st != SS_OK) return st;
+  if (!bytes) {
+    ss_host::set_error("w4a16 workspace: null output pointer");
+    return SS_ERR_INVALID;
+  }
+  *bytes = 0;  // the kernels need no scratch
+  return SS_OK;
+}
+
+extern "C" int ss_w4a16_gemm(const void* x, void* out, const int32_t* qweight, const void* scales,
+                             const int32_t* qzeros, int64_t m, int64_t n, int64_t k, int group_size,
+                             int64_t x_stride, int64_t o_stride, int act_dtype, int scale_dtype,
+                             void* workspace, int64_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  const char* who = "w4a16 gemm";
+  int st = check_w4a16(who, m, n, k, group_size, act_dtype, scale_dtype);
+  if (st != SS_OK) return st;
+  if (m == 0 || n == 0) return SS_OK;
+  if (!x || !out || !qweight || !scales || !qzeros) {
+    ss_host::set_error("%s: null pointer", who);
+    return SS_ERR_INVALID;
+  }
+  if (x_stride < k || o_stride < n) {
+    ss_host::set_error("%s: row strides (x %lld, out %lld) shorter than the rows", who, (long long)x_stride,
+                       (long long)o_stride);
+    return SS_ERR_INVALID;
+  }
+  ss::W4Params p = {};
+  p.x = x;
+  p.out = out;
+  p.qw = (const uint32_t*)qweight;
+  p.sc = scales;
+  p.qz = qzeros;
+  p.x_stride = x_stride;
+  p.o_stride = o_stride;
+  p.m = (int)m;
+  p.n = (int)n;
+  p.k = (int)k;
+  p.g = group_size;
+  p.groups = (int)(k / group_size);
+  p.sdt = scale_dtype;
+  const bool act16 = act_dtype != SS_DTYPE_F32;
+  ss::W4Plan pl = ss::plan_w4a16(m, n, k, group_size, act16);
+  if (pl.fast && (!aligned16(x) || x_stride % 8 != 0 || !aligned16(qweight))) pl.fast = false;
+  hipStream_t s = (hipStream_t)stream;
+  if (!pl.fast) {
+    const int64_t total = m * n;
+    const int64_t blocks = (total + 255) / 256;
+    if (blocks > 0x7fffffff) {
+      ss_host::set_error("%s: generic path grid too large", who);
+      return SS_ERR_UNSUPPORTED;
+    }
+    if (act_dtype == SS_DTYPE_BF16)
+      hipLaunchKernelGGL((ss::w4a16_generic_kernel<ss::bf16_t>), dim3((unsigned)blocks), dim3(256), 0, s, p);
+    else if (act_dtype == SS_DTYPE_F16)
+      hipLaunchKernelGGL((ss::w4a16_generic_kernel<ss::f16_t>), dim3((unsigned)blocks), dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((ss::w4a16_generic_kernel<float>), dim3((unsigned)blocks), dim3(256), 0, s, p);
+    return ss_host::launch_status("w4a16 gemm (generic)");
+  }
+  if (pl.m_blocks > 65535) {
+    ss_host::set_error("%s: %lld activation rows exceed the grid", who, (long long)m);
+    return SS_ERR_UNSUPPORTED;
+  }
+  p.kw = pl.kw;
+  if (act_dtype == SS_DTYPE_BF16) return ss::launch_w4a16_typed<ss::bf16_t>(p, pl, s);
+  return ss::launch_w4a16_typed<ss::f16_t>(p, pl, s);
+}

@@ -6,6 +6,7 @@ from slipstream_amd.kernels.paged_attention import (
     paged_attention_prefill,
     paged_attention_varlen,
 )
+from slipstream_amd.kernels.quant_gemm import w4a16_gemm
 from slipstream_amd.kernels.reshape_and_cache import reshape_and_cache
 
 __all__ = [
@@ -14,4 +15,5 @@ __all__ = [
     "paged_attention_prefill",
     "paged_attention_varlen",
     "reshape_and_cache",
+    "w4a16_gemm",
 ]

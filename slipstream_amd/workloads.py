@@ -223,3 +223,69 @@ def kv_bytes(batch: PagedBatch, unique: bool = False) -> int:
         return sum(batch.ctx_host) * per_token
     shared_tokens = batch.shared_blocks * batch.block_size
     return (shared_tokens + sum(c - shared_tokens for c in batch.ctx_host)) * per_token
+
+
+# ---- W4A16 (C5) ----------------------------------------------------------------------
+
+
+@dataclass
+class W4A16Linear:
+    """One int4 linear in the reference format (quant_ref.py:8-20) plus its activations."""
+
+    x: torch.Tensor  # [M, K] bf16
+    qweight: torch.Tensor  # [N, K/8] int32
+    scales: torch.Tensor  # [N, K/g] fp16
+    qzeros: torch.Tensor  # [N, K/g] int32
+    group_size: int
+
+    @property
+    def m(self) -> int:
+        return int(self.x.shape[0])
+
+    @property
+    def n(self) -> int:
+        return int(self.qweight.shape[0])
+
+    @property
+    def k(self) -> int:
+        return int(self.x.shape[1])
+
+    def weight_bytes(self) -> int:
+        return (self.qweight.numel() * 4 + self.scales.numel() * self.scales.element_size()
+                + self.qzeros.numel() * 4)
+
+
+def pack_int4_torch(q: torch.Tensor) -> torch.Tensor:
+    """``[N, K]`` nibbles -> ``[N, K/8]`` int32, nibble n of word j = q[:, 8j+n] at bit 4n
+    (quant_ref.py:45-60; packed in int64, the int32 keeps the 32-bit pattern)."""
+    n, k = q.shape
+    shifts = torch.arange(0, 32, 4, device=q.device, dtype=torch.int64)
+    words = (q.to(torch.int64).view(n, k // 8, 8) << shifts).sum(dim=-1)
+    return words.to(torch.int32)
+
+
+def w4a16_linear(k: int, n: int, m: int, device="cuda", seed: int = 0, group_size: int = 128,
+                 act: torch.dtype = torch.bfloat16, scale_dtype: torch.dtype = torch.float16) -> W4A16Linear:
+    """C5 operands: q ~ U{0..15}, scales ~ U(0.005, 0.02) in fp16, zero points 8, x ~ N(0, 1)."""
+    device = torch.device(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    q = torch.randint(0, 16, (n, k), generator=gen, device=device, dtype=torch.int32)
+    qweight = pack_int4_torch(q)
+    del q
+    scales = torch.empty((n, k // group_size), device=device, dtype=torch.float32)
+    scales.uniform_(0.005, 0.02, generator=gen)
+    scales = scales.to(scale_dtype)
+    qzeros = torch.full((n, k // group_size), 8, dtype=torch.int32, device=device)
+    x = torch.randn((m, k), generator=gen, device=device, dtype=torch.float32).to(act)
+    return W4A16Linear(x=x, qweight=qweight, scales=scales, qzeros=qzeros, group_size=group_size)
+
+
+def w4a16_reference_fp32(lin: W4A16Linear) -> torch.Tensor:
+    """fp32 dequant-then-matmul on the operands' device: ``x.float() @ ((q - z) * s).T``."""
+    n, k, g = lin.n, lin.k, lin.group_size
+    shifts = torch.arange(0, 32, 4, device=lin.qweight.device, dtype=torch.int64)
+    words = lin.qweight.to(torch.int64) & 0xFFFFFFFF
+    q = ((words.unsqueeze(-1) >> shifts) & 0xF).view(n, k // g, g).float()
+    w = (q - lin.qzeros.float().unsqueeze(-1)) * lin.scales.float().unsqueeze(-1)
+    return lin.x.float() @ w.view(n, k).t()

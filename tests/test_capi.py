@@ -22,7 +22,8 @@ def declared_functions() -> list[str]:
 def test_header_declares_entry_points():
     names = declared_functions()
     for required in ("ss_reshape_and_cache", "ss_paged_attention", "ss_paged_attention_varlen",
-                     "ss_paged_attention_workspace_size", "ss_status_string", "ss_last_error"):
+                     "ss_paged_attention_workspace_size", "ss_status_string", "ss_last_error",
+                     "ss_w4a16_gemm", "ss_w4a16_workspace_size"):
         assert required in names
 
 
@@ -65,3 +66,22 @@ def test_argument_errors_need_no_device():
     st = lib.ss_reshape_and_cache(None, None, None, None, None, 0, 0, 8, 128, 16, 0, z, z, z, 2, None)
     assert st == _ffi.SS_OK
     assert isinstance(ctypes.c_int(st).value, int)
+
+
+def test_w4a16_argument_errors_need_no_device():
+    """Format checks of quant_ref.py:38-42 happen on the host: bad group sizes are SS_ERR_INVALID."""
+    from slipstream_amd import _ffi
+
+    lib = _ffi.lib()
+    out = ctypes.c_int64(-1)
+    assert lib.ss_w4a16_workspace_size(4, 64, 256, 12, _ffi.SS_DTYPE_BF16, ctypes.byref(out)) == _ffi.SS_ERR_INVALID
+    assert b"multiple of 8" in lib.ss_last_error()
+    assert lib.ss_w4a16_workspace_size(4, 64, 100, 32, _ffi.SS_DTYPE_BF16, ctypes.byref(out)) == _ffi.SS_ERR_INVALID
+    assert lib.ss_w4a16_workspace_size(1, 4096, 4096, 128, _ffi.SS_DTYPE_BF16, ctypes.byref(out)) == _ffi.SS_OK
+    assert out.value >= 0
+    st = lib.ss_w4a16_gemm(None, None, None, None, None, 0, 8, 256, 128, 256, 8, _ffi.SS_DTYPE_BF16,
+                           _ffi.SS_DTYPE_F16, None, 0, None)
+    assert st == _ffi.SS_OK  # empty batch touches nothing
+    st = lib.ss_w4a16_gemm(None, None, None, None, None, 1, 8, 256, 128, 256, 8, _ffi.SS_DTYPE_BF16,
+                           7, None, 0, None)
+    assert st == _ffi.SS_ERR_UNSUPPORTED
