@@ -41,6 +41,9 @@ struct W4Params {
 };
 
 constexpr int kMaxKW = 8;
+// Cache policy of the weight loads: non-temporal (every weight is read once per call;
+// streaming without cache allocation measured ~14 % more bandwidth on gfx950).
+constexpr int kNonTemporal = 2;
 
 template <typename T>
 struct W4Elem;
@@ -161,11 +164,11 @@ __global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
 #pragma unroll
       for (int ns = 0; ns < NS; ++ns) {
         if (WIDE) {
-          wb.w[ns][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, w_off[ns], kk / 2, 0));
+          wb.w[ns][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, w_off[ns], kk / 2, kNonTemporal));
         } else {
 #pragma unroll
           for (int s = 0; s < 4; ++s)
-            wb.w[ns][it][s] = __builtin_amdgcn_raw_buffer_load_b32(rw, w_off[ns], kk / 2 + 16 * s, 0);
+            wb.w[ns][it][s] = __builtin_amdgcn_raw_buffer_load_b32(rw, w_off[ns], kk / 2 + 16 * s, kNonTemporal);
         }
       }
     }
