@@ -42,8 +42,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the host-side reference timing")
     ap.add_argument("--skip-extra", action="store_true", help="headline only (no packed / prefix lines)")
-    ap.add_argument("--only", choices=["all", "w4a16"], default="all",
-                    help="w4a16: run the C5 section alone and print it (profiling aid)")
+    ap.add_argument("--only", choices=["all", "w4a16", "copy"], default="all",
+                    help="w4a16: run the C5 section alone; copy: 1 GiB device copies of known size, the "
+                         "calibration kernel for the FETCH_SIZE/WRITE_SIZE counters (profiling aids)")
     return ap.parse_args()
 
 
@@ -115,6 +116,23 @@ def prefill_flops(b) -> float:
             prior = ctx - ql
             f += 4.0 * b.n_q * b.head_dim * (ql * prior + ql * (ql + 1) / 2)
     return f
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_decode_c2_hbm_traffic.json")
+
+
+def measured_traffic(bytes_per_launch: int):
+    """HBM bytes per decode launch from the committed FETCH_SIZE / WRITE_SIZE passes
+    (rocprofv3 --pmc, one counter per run, scaled by a copy kernel's readings), used
+    only when they were taken on this exact workload (same algorithmic bytes)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None, None
+    if rec.get("algorithmic_bytes_per_launch") != bytes_per_launch:
+        return None, None
+    return int(rec["hbm_bytes_per_launch"]), os.path.relpath(TRAFFIC_FILE, ROOT)
 
 
 def cpu_baseline(b, seed: int) -> dict:
@@ -261,6 +279,14 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    if args.only == "copy":  # counter calibration: a plain copy of known size
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        src.fill_(1)
+        dst = torch.empty_like(src)
+        ms, _ = time_loop(lambda: dst.copy_(src), 5, 1)
+        print(json.dumps({"copy_bytes_read": src.numel(), "copy_bytes_written": dst.numel(),
+                          "us_per_copy": round(ms * 1e3, 1)}), flush=True)
+        return 0
     if args.only == "w4a16":  # profiling aid: the C5 section alone
         print(json.dumps({"w4a16": w4a16_section(dev, args.steps, args.warmup)}), flush=True)
         return 0
@@ -280,6 +306,7 @@ def main() -> int:
     ms_step, wall_step = time_loop(step, args.steps, args.warmup)
     ms_attn, _ = time_loop(attn, args.steps, args.warmup)
     value = nbytes["step"] / (ms_step * 1e-3) / 1e9
+    traffic, traffic_src = measured_traffic(nbytes["attention"])
     attn_gbs = nbytes["attention"] / (ms_attn * 1e-3) / 1e9
 
     result = {
@@ -317,7 +344,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "bytes_per_launch": nbytes["attention"],
             "us_per_launch": round(ms_attn * 1e3, 2),
         },

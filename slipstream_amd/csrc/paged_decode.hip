@@ -235,10 +235,13 @@ __device__ __forceinline__ void compute_pair(const AttnParams& p, const DecodeTi
 // constant of the kernel, so a pair costs no vector address arithmetic.
 typedef const __attribute__((address_space(4))) int32_t* ConstTable;
 
-// Cache policy of the K/V page loads: non-temporal. Each page is read once per step;
-// streaming it without allocating in the caches measured ~14 % more bandwidth on
-// gfx950 than the default policy for this access pattern.
+// Cache policy of the K/V page loads (buffer-load aux bits). A page read once per step
+// streams best non-temporally: without allocating in the caches it measured ~14 % more
+// bandwidth on gfx950 than the default policy. Pages shared by several sequences (a
+// common prefix) are read once per sequence, and there the default policy lets the
+// re-reads hit the 256 MB MALL; the host picks the policy from the pool's size.
 constexpr int kNonTemporal = 2;
+constexpr int kDefaultPolicy = 0;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char* base, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, bytes, 0x00020000);
@@ -263,7 +266,7 @@ __device__ __forceinline__ void fetch_phys(const AttnParams& p, const ScalarTabl
   }
 }
 
-template <typename T, int D>
+template <typename T, int D, int AUX>
 __device__ __forceinline__ void load_pair_scalar(const AttnParams& p, const ScalarTableCtx& c, int pi,
                                                  const int (&ph)[2], int voff_k, const int (&voff_v)[4],
                                                  DecodeTile<T, D>& t) {
@@ -286,19 +289,20 @@ __device__ __forceinline__ void load_pair_scalar(const AttnParams& p, const Scal
     const __amdgpu_buffer_rsrc_t rv = tile_rsrc(c.vplane + off, bytes);
 #pragma unroll
     for (int s = 0; s < Tile::KS; ++s)
-      t.k[x][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, voff_k + 64 * s, 0, kNonTemporal));
+      t.k[x][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, voff_k + 64 * s, 0, AUX));
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
       for (int mt = 0; mt < Tile::MT; ++mt)
         t.v[mt][4 * x + e] =
-            __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff_v[e] + 256 * mt, 0, kNonTemporal));
+            __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff_v[e] + 256 * mt, 0, AUX));
   }
 }
 
 // STAB: scalar block-table path (block_size >= 16); otherwise every lane looks up
-// its own block (block_size 4 and 8 put several blocks in one 16-token tile).
-template <typename T, int D, bool STAB>
+// its own block (block_size 4 and 8 put several blocks in one 16-token tile). AUX: the
+// page-load cache policy of the STAB path.
+template <typename T, int D, bool STAB, int AUX>
 __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
   typedef DecodeTile<T, D> Tile;
   __shared__ int s_red[16];
@@ -462,7 +466,7 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
     DecodeTile<T, D> ta, tb;
     int pha[2], phb[2], phn[2];
     fetch_phys(p, tc, pos - c, pha);
-    load_pair_scalar<T, D>(p, tc, pos - c, pha, voff_k, voff_v, ta);
+    load_pair_scalar<T, D, AUX>(p, tc, pos - c, pha, voff_k, voff_v, ta);
     while (true) {
       const int seg0 = pos - c;
       const int seg1 = min(e_w - c, nbp);
@@ -508,7 +512,7 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
         int ph[2];
         ph[0] = in_seg ? ph_in[0] : (look ? phn[0] : -1);
         ph[1] = in_seg ? ph_in[1] : (look ? phn[1] : -1);
-        load_pair_scalar<T, D>(p, tg, in_seg ? pi_ + 1 : 0, ph, voff_k, voff_v, dst);
+        load_pair_scalar<T, D, AUX>(p, tg, in_seg ? pi_ + 1 : 0, ph, voff_k, voff_v, dst);
         load_q(look ? nb : b, look ? qoff_n : qoff, look ? j_n : j, look ? hq_n : hq, look && ok_n, qn);
       };
 
@@ -689,6 +693,10 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const AttnParams p, i
 
 // ---- host side -------------------------------------------------------------
 
+// K+V bytes of one layer's pool up to which the page loads keep the default cache
+// policy (the MI355X MALL is 256 MB; leave room for the queries and workspace).
+constexpr int64_t kMallReuseBytes = 192ll << 20;
+
 static int heads_per_wg(int n_kv) {
   for (int d = 8; d >= 1; --d)
     if (n_kv % d == 0) return d;
@@ -698,7 +706,7 @@ static int heads_per_wg(int n_kv) {
 template <typename T, int D>
 static int decode_resident_wgs(int hpw) {
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<T, D, true>, hpw * 64, 0) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<T, D, true, kNonTemporal>, hpw * 64, 0) !=
           hipSuccess ||
       per_cu < 1)
     per_cu = 1;
@@ -766,11 +774,17 @@ static int launch_decode_typed(AttnParams p, int max_query_len, char* ws, int64_
   }
   // the scalar-table walker needs block_size >= 16 (one block per 16-token tile); at
   // head_dim 256 its two pairs in flight exceed the register file, so it takes the
-  // per-lane path there
-  if (p.block_size >= 16 && D <= 128)
-    hipLaunchKernelGGL((decode_kernel<T, D, true>), dim3(g.n_wg), dim3(g.hpw * 64), 0, stream, p);
+  // per-lane path there. Pools whose K and V planes of this layer fit the MALL use the
+  // default cache policy, so pages shared between sequences are re-read from it.
+  const int64_t pool_bytes = 2 * (int64_t)p.num_blocks * p.c_sb * (int64_t)sizeof(T);
+  if (p.block_size >= 16 && D <= 128 && pool_bytes > kMallReuseBytes)
+    hipLaunchKernelGGL((decode_kernel<T, D, true, kNonTemporal>), dim3(g.n_wg), dim3(g.hpw * 64), 0, stream, p);
+  else if (p.block_size >= 16 && D <= 128)
+    hipLaunchKernelGGL((decode_kernel<T, D, true, kDefaultPolicy>), dim3(g.n_wg), dim3(g.hpw * 64), 0, stream,
+                       p);
   else
-    hipLaunchKernelGGL((decode_kernel<T, D, false>), dim3(g.n_wg), dim3(g.hpw * 64), 0, stream, p);
+    hipLaunchKernelGGL((decode_kernel<T, D, false, kDefaultPolicy>), dim3(g.n_wg), dim3(g.hpw * 64), 0, stream,
+                       p);
   int st = ss_host::launch_status("paged attention decode");
   if (st != SS_OK) return st;
   hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(g.n_wg + p.batch), dim3(256), 0, stream, p, g.n_wg);

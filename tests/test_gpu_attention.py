@@ -207,6 +207,24 @@ def test_decode_is_invariant_to_block_permutation(device):
     assert torch.equal(out1, out2)
 
 
+@pytest.mark.parametrize("tq", [1, 3])
+def test_decode_cache_policies_agree(device, tq):
+    """The page loads stream non-temporally when one layer's K+V pool exceeds 192 MiB and
+    keep the default cache policy below that; the same batch in a small and in a 256 MiB
+    pool gives bit-identical outputs (and matches the oracle)."""
+    b = workloads.build_batch([3000, 700, 33, 1500, 16, 257], [tq] * 6, n_q=32, n_kv=8, head_dim=128,
+                              block_size=16, dtype=torch.bfloat16, device=device, seed=23)
+    nb = b.kv_cache.shape[2]
+    big = torch.zeros((1, 2, 4096) + tuple(b.kv_cache.shape[3:]), dtype=b.kv_cache.dtype, device=device)
+    big[:, :, :nb] = b.kv_cache
+    assert big.numel() * big.element_size() > (192 << 20) > b.kv_cache.numel() * b.kv_cache.element_size()
+    q = b.padded_q()
+    out_small = paged_attention_decode(q, b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
+    out_big = paged_attention_decode(q, big, b.block_tables, b.context_lens, 0, b.scale, 16)
+    assert torch.equal(out_small, out_big)
+    assert_attn_close(out_big, _oracle_padded(b), f"tq={tq}")
+
+
 def test_decode_shared_prefix_equals_private_copies(device):
     """Prefix config (C4 shape, reduced batch): tables sharing 128 blocks == private copies."""
     b = workloads.prefix_share(device=device, seed=2, batch=16)
