@@ -80,11 +80,16 @@ void fill_common(AttnParams& p, const void* q, void* out, const void* k_cache, c
 int run(AttnParams& p, int dtype, int head_dim, int max_query_len, void* workspace, int64_t ws_bytes,
         hipStream_t stream, bool decode_rows, bool prefill_rows) {
   p.rmax = ss::decode_rows_for(max_query_len, p.n_rep);
-  if (decode_rows) {
-    int st = ss::launch_decode(p, dtype, head_dim, max_query_len, (char*)workspace, ws_bytes, stream);
-    if (st != SS_OK) return st;
-  }
-  if (prefill_rows) return ss::launch_prefill(p, dtype, head_dim, max_query_len, stream);
+  auto decode = [&](hipStream_t s) {
+    return ss::launch_decode(p, dtype, head_dim, max_query_len, (char*)workspace, ws_bytes, s);
+  };
+  auto prefill = [&](hipStream_t s) { return ss::launch_prefill(p, dtype, head_dim, max_query_len, s); };
+  // A packed step has both kinds of rows: the decode part is bound by HBM and the
+  // prefill part by the matrix cores, and they write disjoint output rows, so the
+  // prefill runs on a side stream next to the decode.
+  if (decode_rows && prefill_rows) return ss_host::run_concurrently(stream, prefill, decode);
+  if (decode_rows) return decode(stream);
+  if (prefill_rows) return prefill(stream);
   return SS_OK;
 }
 

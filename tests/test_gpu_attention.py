@@ -273,6 +273,50 @@ def test_prefill_fp16_head_dim_64(device):
     assert_attn_close(out, ref, "prefill fp16 D64")
 
 
+@pytest.mark.parametrize("block_size", [8, 32, 64])
+def test_prefill_block_sizes(device, block_size):
+    """Tiles of 64 keys cover several 16-key groups of one block (32, 64) or take the
+    per-lane kernel (8); chunk lengths cut tiles and blocks at odd places."""
+    print(f"prefill block_size={block_size}", flush=True)
+    b = workloads.build_batch([77, 400, 1031], [77, 77, 77], n_q=32, n_kv=8, head_dim=128,
+                              block_size=block_size, dtype=torch.bfloat16, device="cpu", seed=block_size)
+    ref = _oracle_padded(b)
+    _to(b, device)
+    out = paged_attention_prefill(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale,
+                                  block_size)
+    assert_attn_close(out, ref, f"prefill bs={block_size}")
+
+
+def test_prefill_table_holes(device):
+    """Absent blocks (negative, past the pool) inside a chunk's prior context and inside
+    the chunk itself are masked for every query row."""
+    b = workloads.build_batch([300, 260], [100, 100], n_q=32, n_kv=8, head_dim=128, block_size=16,
+                              dtype=torch.bfloat16, device="cpu", seed=31)
+    tables = [list(t) for t in b.tables_host]
+    tables[0][2] = -1          # keys 32..47: prior context
+    tables[0][15] = 10_000     # keys 240..255: inside the chunk
+    tables[1][0] = -3          # the first block
+    width = b.block_tables.shape[1]
+    bt = torch.full((2, width), -1, dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, : len(t)] = torch.tensor(t, dtype=torch.int32)
+    b.block_tables = bt
+    ref = ora.paged_attention(f64(b.padded_q()), f64(b.kv_cache), tables_array(tables, width),
+                              np.array(b.ctx_host), 0, b.scale, 16)
+    _to(b, device)
+    out = paged_attention_prefill(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
+    assert_attn_close(out, ref, "prefill holes")
+
+
+def test_prefill_head_dim_256(device):
+    b = workloads.build_batch([40, 300], [40, 40], n_q=8, n_kv=2, head_dim=256, block_size=16,
+                              dtype=torch.bfloat16, device="cpu", seed=256)
+    ref = _oracle_padded(b)
+    _to(b, device)
+    out = paged_attention_prefill(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
+    assert_attn_close(out, ref, "prefill D256")
+
+
 # ---------------------------------------------------------------- packed varlen
 
 
@@ -332,3 +376,35 @@ def test_varlen_full_mixed_step_subset_checked(device):
         kk, vv, valid = ora.gather_kv(pool, 0, np.array(tables[k]), b.ctx_host[i], 16)
         ref = ora.attend(qb, kk, vv, valid, b.ctx_host[i], b.scale)
         assert_attn_close(out[s1 - m:s1], ref, f"C3 seq {i}")
+
+
+def test_varlen_packed_step_graph_replays(device):
+    """The packed step forks its prefill onto a side stream and joins it back with events;
+    captured in a HIP graph (after an eager warm-up), every replay equals the eager step."""
+    ctx, ql = workloads.mixed_step_lengths(seed=9, n_prefill=2, chunk=80, n_decode=20)
+    b = workloads.build_batch(ctx, ql, n_q=32, n_kv=8, head_dim=128, block_size=16, dtype=torch.bfloat16,
+                              device=device, seed=9)
+
+    def step():
+        reshape_and_cache(b.k_new, b.v_new, b.kv_cache, b.slot_mapping, 0, 16)
+        return paged_attention_varlen(b.q, b.kv_cache, b.block_tables, b.cu_seqlens, b.context_lens, 0,
+                                      b.scale, 16, b.max_query_len)
+
+    eager = step().clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out = step()
+    for rep in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep}"
+        again = step()  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager)
