@@ -26,6 +26,9 @@ namespace {
 __device__ __attribute__((aligned(16))) uint32_t g_zero_row_p[128];
 
 constexpr int kPrefillWaves = 4;
+// Slack (log2 units) by which a row's max may exceed the running max before the
+// running state is rescaled (tiled prefill kernel).
+constexpr float kRescaleSlack = 8.0f;
 constexpr int kKeyTile = 32;
 
 template <typename T, int D, int NT>
@@ -262,10 +265,13 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnParams p) {
 //  - the V^T operand of O^T += V^T P^T comes from ds_read_b64_tr_b16: within
 //    each 16-lane group, lane i receives element i%4 of the 8-byte reads of
 //    lanes i/4 + 4e (e = 0..3). Lane s of group G reads key 4G + s/4 (+16 for
-//    the second read) at d = (D/4)(s%4) + 4*dt, so lane i of the result holds
-//    d = (D/4)(i/4) + 4*dt + i%4 for keys 4G..4G+3 and 16+4G..16+4G+3 -- the
-//    key order of the P^T operand taken straight from the S^T accumulator,
-//    and a d order that leaves each lane D/4 consecutive outputs of its row.
+//    the second read) at d = (D/4) q + 4 (dt ^ (q & 1)), q = s%4, so lane i of
+//    the result holds d = (D/4)(i/4) + 4 (dt ^ (i/4 & 1)) + i%4 for keys
+//    4G..4G+3 and 16+4G..16+4G+3 -- the key order of the P^T operand taken
+//    straight from the S^T accumulator, and a d order that leaves each lane
+//    D/4 consecutive outputs of its row. The dt ^ (q & 1) term sends lanes of
+//    odd q to the other 8-byte half of their chunk, which keeps the reads free
+//    of LDS bank conflicts.
 //  - software pipeline: a step runs the QK product of the next tile next to
 //    the softmax of the current one (independent work, one branch-free block).
 //  - softmax: the max is taken over raw scores and the scale applied inside the
@@ -344,8 +350,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int ROWS = 128;
   constexpr int XS = 4;              // 16-key subtiles of a tile
   constexpr int LPG = C::NI;         // DMA instructions per wave and load group
-  char* const kring = s_tile_stages;                  // K tile j in slot j % 3
-  char* const vring = s_tile_stages + 3 * C::PLANE;   // V tile j in slot j % 3
+  // V ring first: the V reads' stage, row and d offsets then all fit the 16-bit
+  // immediate offset of the LDS instructions (the K reads use per-lane bases)
+  char* const vring = s_tile_stages;                  // V tile j in slot j % 3
+  char* const kring = s_tile_stages + 3 * C::PLANE;   // K tile j in slot j % 3
 
   const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   int qlen;
@@ -465,17 +473,35 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const u32x4 ones = {kOnePair, kOnePair, kOnePair, kOnePair};
   const float ninf = -__builtin_inff();
 
-  // S^T of a tile (A = K rows from LDS, B = Q^T)
-  auto qk = [&](const char* kst, f32x4 (&sacc)[NT][XS]) {
-    const LdsBytes ks = (LdsBytes)kst;
+  // Per-lane LDS read pointers into ring slot 0, the same for every tile (the
+  // swizzle of K rows 16x + n and of V rows 32kk + r0 (+16) does not depend on
+  // x or kk): slot, subtile and row offsets are then instruction immediates.
+  LdsBytes kptr[C::KS];
+#pragma unroll
+  for (int s = 0; s < C::KS; ++s) kptr[s] = (LdsBytes)kring + (n * C::ROWB + chunk_slot<T, D>(n, 4 * s + g) * 16);
+  LdsBytes vptr[C::DT];
+  {
+    const int sl = lane & 15, G = lane >> 4;
+    const int r0 = 4 * G + (sl >> 2);
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) {
+      // d-quad of this lane in d-tile dt: (D/4) q + 4 (dt ^ (q & 1)), q = sl & 3.
+      // Lanes of odd q read the other 8-byte half of their 16-byte chunk, so the
+      // 32 lanes an LDS cycle serves cover all 64 banks once.
+      const int q = sl & 3;
+      const int dq = (D / 4) * q + 4 * (dt ^ (q & 1));
+      vptr[dt] = (LdsBytes)vring + (r0 * C::ROWB + chunk_slot<T, D>(r0, dq >> 3) * 16 + 2 * (dq & 7));
+    }
+  }
+
+  // S^T of the tile in K ring slot r (A = K rows from LDS, B = Q^T)
+  auto qk = [&](int r, f32x4 (&sacc)[NT][XS]) {
 #pragma unroll
     for (int x = 0; x < XS; ++x) {
       u32x4 ka[C::KS];
-      const int row = 16 * x + n;
 #pragma unroll
       for (int s = 0; s < C::KS; ++s)
-        ka[s] = *(const __attribute__((address_space(3))) u32x4*)(ks + (row * C::ROWB +
-                                                                  chunk_slot<T, D>(row, 4 * s + g) * 16));
+        ka[s] = *(const __attribute__((address_space(3))) u32x4*)(kptr[s] + (r * C::PLANE + 16 * x * C::ROWB));
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         sacc[nt][x] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -509,7 +535,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int i = 1; i < 4 * XS; ++i) mx = fmaxf(mx, sv[i]);
       mx = max_across_rows(mx);
-      mnew[nt] = fmaxf(mrow[nt], mx * cscale);
+      // the running max is only raised when some row's max outgrew it by more
+      // than kRescaleSlack (log2 units): p then stays below 2^kRescaleSlack, and
+      // the rescale of the accumulators is rare after the first tiles
+      const float mcand = fmaxf(mrow[nt], mx * cscale);
+      mnew[nt] = __any(mcand > mrow[nt] + kRescaleSlack) ? mcand : mrow[nt];
       float pv[4 * XS];
 #pragma unroll
       for (int i = 0; i < 4 * XS; ++i) pv[i] = fast_exp2(__builtin_fmaf(sv[i], cscale, -mnew[nt]));
@@ -533,21 +563,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   };
   // O^T += V^T P^T from a V tile
-  auto pv_product = [&](const u32x4 (&pop)[NT][XS / 2], const char* vst) {
-    const LdsBytes vs = (LdsBytes)vst;
-    const int sl = lane & 15, G = lane >> 4;
+  auto pv_product = [&](const u32x4 (&pop)[NT][XS / 2], int r) {
 #pragma unroll
     for (int kk = 0; kk < XS / 2; ++kk) {
-      const int row1 = 32 * kk + 4 * G + (sl >> 2);
-      const int row2 = row1 + 16;
 #pragma unroll
       for (int dt = 0; dt < C::DT; ++dt) {
-        const int c = ((D / 4) * (sl & 3) + 4 * dt) >> 3;
-        const int byte = 8 * (dt & 1);
-        const int o1 = row1 * C::ROWB + chunk_slot<T, D>(row1, c) * 16 + byte;
-        const int o2 = row2 * C::ROWB + chunk_slot<T, D>(row2, c) * 16 + byte;
-        const tr16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tr16x4*)(vs + o1));
-        const tr16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tr16x4*)(vs + o2));
+        const int o1 = r * C::PLANE + 32 * kk * C::ROWB;
+        const int o2 = o1 + 16 * C::ROWB;
+        const tr16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tr16x4*)(vptr[dt] + o1));
+        const tr16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tr16x4*)(vptr[dt] + o2));
         const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
         const u32x4 va = {l2[0], l2[1], h2[0], h2[1]};
 #pragma unroll
@@ -559,8 +583,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
   // one tile: QK of the next tile and the softmax of this one in one branch-free
   // block (independent work the scheduler can interleave), then the rescale and PV
-  auto tile_step = [&](int t, int vbits, const char* knext, const f32x4 (&scur)[NT][XS], f32x4 (&snext)[NT][XS],
-                       const char* vst) {
+  auto tile_step = [&](int t, int vbits, int knext, const f32x4 (&scur)[NT][XS], f32x4 (&snext)[NT][XS],
+                       int vslot) {
     float mnew[NT];
     u32x4 pop[NT][XS / 2];
     if (vbits == 0xF && (t + 1) * C::KT <= wave_lim) {
@@ -571,7 +595,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       softmax_p(std::true_type{}, t, vbits, scur, mnew, pop);
     }
     advance(mnew);
-    pv_product(pop, vst);
+    pv_product(pop, vslot);
   };
 
   // Software pipeline. DMA group j (j >= 1) is {K tile j, V tile j-1}; group 0 is
@@ -631,7 +655,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // in group 1, so it waits for the same count)
     wait_vm<2 * C::NI>();
     __syncthreads();
-    qk(kring, sa);
+    qk(0, sa);
     // K slot of tile t+1 = (t+1) % 3, V slot of tile t = t % 3
     auto step = [&](int t, int r, int& ph_r, int& vb_r, int ph_v, f32x4 (&scur)[NT][XS], f32x4 (&snext)[NT][XS]) {
       wait_vm<LPG>();
@@ -641,7 +665,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (k_loader) issue(t + 3, ph_r, kplane, kring + r * C::PLANE);
       if (v_loader) issue(t + 2, ph_v, vplane, vring + ((r + 2) % 3) * C::PLANE);
       fetch(t + 4);
-      tile_step(t, vcur, kring + ((r + 1) % 3) * C::PLANE, scur, snext, vring + r * C::PLANE);
+      tile_step(t, vcur, (r + 1) % 3, scur, snext, r);
     };
     for (int t = 0; t < ntiles; t += 3) {
       step(t, 0, ph0, vb0, ph2, sa, sb);
@@ -658,7 +682,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // no LDS write may land after the workgroup ends
   wait_vm<0>();
 
-  // each lane holds D/4 consecutive outputs, d = (D/4) g + 4 dt + e
+  // each lane holds D/4 consecutive outputs of its row: acc[dt][e] is
+  // d = (D/4) g + 4 (dt ^ (g & 1)) + e, so 16-byte store w takes d-tiles 2w and
+  // 2w+1, swapped for odd g
+  const bool swap = g & 1;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const float lt = lsum[nt][0];
@@ -670,7 +697,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       T* orow = (T*)p.out + (int64_t)b * p.o_sb + (qoff + j) * p.o_st + (int64_t)hq * p.o_sh + (D / 4) * g;
 #pragma unroll
       for (int w = 0; w < C::DT / 2; ++w) {
-        const f32x4 o0 = acc[nt][2 * w] * inv, o1 = acc[nt][2 * w + 1] * inv;
+        const f32x4 x0 = swap ? acc[nt][2 * w + 1] : acc[nt][2 * w];
+        const f32x4 x1 = swap ? acc[nt][2 * w] : acc[nt][2 * w + 1];
+        const f32x4 o0 = x0 * inv, o1 = x1 * inv;
         const u32x4 o = {Elem<T>::pack2(o0[0], o0[1]), Elem<T>::pack2(o0[2], o0[3]), Elem<T>::pack2(o1[0], o1[1]),
                          Elem<T>::pack2(o1[2], o1[3])};
         store16(orow + 8 * w, o);
