@@ -70,6 +70,21 @@ __device__ __forceinline__ float load_scale(const void* s, int64_t i, int sdt) {
   return ((const float*)s)[i];
 }
 
+// Scales read without branching on their dtype around the load (a load inside a
+// dtype branch makes the compiler wait for every outstanding load at the join):
+// the aligned dword holding scale gi, through a descriptor bounded by the array
+// (bytes past its end read as zero), shifted so the scale's bits are the low ones;
+// decoded afterwards.
+__device__ __forceinline__ uint32_t scale_bits(__amdgpu_buffer_rsrc_t rs, int64_t gi, int esize) {
+  const int off = (int)(gi * esize);
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, off & ~3, 0, 0) >> (8 * (off & 2));
+}
+__device__ __forceinline__ float decode_scale(uint32_t bits, int sdt) {
+  const float f16 = (float)__builtin_bit_cast(f16_t, (uint16_t)(bits & 0xFFFFu));
+  const float b16 = __builtin_bit_cast(float, bits << 16);
+  return sdt == SS_DTYPE_F16 ? f16 : (sdt == SS_DTYPE_BF16 ? b16 : __builtin_bit_cast(float, bits));
+}
+
 // A constant held in a VGPR. gfx9 VOP3 instructions take no literal and read at most
 // one SGPR, so (w & mask) | magic becomes one v_and_or_b32 only when the magic word
 // already sits in a VGPR (the mask goes to the SGPR slot); otherwise it takes a
@@ -90,6 +105,20 @@ __device__ __forceinline__ u32x4 nibbles_to_operand(uint32_t w, uint32_t magic) 
 __device__ __forceinline__ u32x4 permute_x(u32x4 d) {
   return u32x4{pick_halves<0, 0>(d[0], d[2]), pick_halves<1, 1>(d[0], d[2]), pick_halves<0, 0>(d[1], d[3]),
                pick_halves<1, 1>(d[1], d[3])};
+}
+
+// acc + a.lo * b.lo + a.hi * b.hi over packed 16-bit pairs, fp32 accumulation
+template <typename T>
+__device__ __forceinline__ float dot2_acc(uint32_t a, uint32_t b, float acc);
+template <>
+__device__ __forceinline__ float dot2_acc<bf16_t>(uint32_t a, uint32_t b, float acc) {
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(s16x2, a), __builtin_bit_cast(s16x2, b), acc, false);
+}
+template <>
+__device__ __forceinline__ float dot2_acc<f16_t>(uint32_t a, uint32_t b, float acc) {
+  typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h16x2, a), __builtin_bit_cast(h16x2, b), acc, false);
 }
 
 // Raw buffer resource over [base, base + bytes): loads past the end return 0, and a
@@ -382,10 +411,148 @@ __global__ __launch_bounds__(256) void w4a16_generic_kernel(const W4Params p) {
 
 // ---- host side -------------------------------------------------------------
 
+// Batch-1 (decode) W4A16 GEMV, shaped for HBM bandwidth rather than MFMA tiles.
+// A workgroup owns 16 weight rows; each of its waves owns one contiguous slice of
+// K (128 IT keys). Four consecutive lanes share a row and read its 64 contiguous
+// bytes (128 keys, one 16-byte load each), so a wave's load moves 16 full 64-byte
+// row segments; every wave issues all its loads up front, so the whole matrix is
+// requested at once. The activation rows
+// are staged in LDS once per workgroup, permuted to the nibble order, with the
+// sum of every 32 keys. Per 16-byte piece (32 keys of one row, one quantisation
+// group as g % 32 == 0) a lane computes G = sum x (MAGIC + q) with v_dot2 and
+// folds s * (G - (MAGIC + z) * X); the four lanes of a row add by DPP, the waves'
+// slices add in LDS in wave order (no atomics: the result does not depend on
+// timing).
+//
+// LDS: x [MR][K] permuted | chunk sums [K/32][MR] floats | slice partials [waves][16][MR] floats
+// MR: activation rows held (the kernel is used with MR = 1). IT: 128-key iterations
+// per wave (8: 1024-key slices for K <= 8192; 16: 2048-key slices for K <= 16384),
+// so a workgroup has at most 8 waves.
+template <typename T, int MR, int IT>
+__global__ __launch_bounds__(512) void w4a16_gemv_kernel(const W4Params p) {
+  typedef W4Elem<T> E;
+  extern __shared__ __attribute__((aligned(16))) char s_dyn[];
+  const int K = p.k;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const int n0 = blockIdx.x * 16;
+  const int row = n0 + (lane >> 2), pq = lane & 3;
+  const int k0 = wave * 128 * IT;
+
+  // Load order matters: the vector-memory counter retires loads in order, so the
+  // two activation pieces each thread stages are requested first, then this wave's
+  // weights (8 x 16 bytes per lane), then their scales and zero points. The staging
+  // below waits for the activations only, and iteration i of the dot products for
+  // weight load i only, so the arithmetic overlaps the weight stream.
+  // blockDim = 64 * K / (128 IT), so every thread stages exactly MR * IT / 4 pieces of
+  // 8 keys.
+  T* s_x = (T*)s_dyn;
+  float* s_xs = (float*)(s_dyn + (size_t)MR * K * sizeof(T));
+  float* s_part = s_xs + (size_t)(K / 32) * MR;
+  u32x4 xin[MR * IT / 4];
+#pragma unroll
+  for (int e2 = 0; e2 < MR * IT / 4; ++e2) {
+    const int e = threadIdx.x + e2 * blockDim.x;
+    const int r = e / (K / 8), c8 = e - r * (K / 8);
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    xin[e2] = r < p.m ? load16((const T*)p.x + (int64_t)r * p.x_stride + 8 * c8) : z;
+  }
+  // this wave's weights, non-temporal; one descriptor over the workgroup's rows
+  // (rows past N read as zero)
+  const bool rok = row < p.n;
+  const int live_rows = min(16, p.n - n0);
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(p.qw + (int64_t)n0 * (K / 8), (uint32_t)live_rows * (uint32_t)(K / 2));
+  const int vrow = (lane >> 2) * (K / 2) + (k0 + 32 * pq) / 2;
+  u32x4 wv[IT];
+#pragma unroll
+  for (int i = 0; i < IT; ++i)
+    wv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, vrow, 64 * i, kNonTemporal));
+  const int esize = p.sdt == SS_DTYPE_F32 ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.sc, (uint32_t)((int64_t)p.n * p.groups * esize));
+  const __amdgpu_buffer_rsrc_t rzp = buffer_rsrc(p.qz, (uint32_t)((int64_t)p.n * p.groups * 4));
+  uint32_t sb[IT];
+  int zi[IT];
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int64_t gi = (int64_t)(rok ? row : 0) * p.groups + (k0 + 128 * i + 32 * pq) / p.g;
+    sb[i] = scale_bits(rsc, gi, esize);
+    zi[i] = __builtin_amdgcn_raw_buffer_load_b32(rzp, (int)(gi * 4), 0, 0);
+  }
+
+  // activations -> LDS (permuted to the nibble order), then per-32-key sums
+#pragma unroll
+  for (int e2 = 0; e2 < MR * IT / 4; ++e2) {
+    const int e = threadIdx.x + e2 * blockDim.x;
+    const int r = e / (K / 8), c8 = e - r * (K / 8);
+    store16(s_x + (size_t)r * K + 8 * c8, permute_x(xin[e2]));
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < MR * (K / 32); e += blockDim.x) {
+    const int r = e / (K / 32), c = e - r * (K / 32);
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 v = load16(s_x + (size_t)r * K + 32 * c + 8 * j);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) sum += E::to_f32(v[h] & 0xFFFFu) + E::to_f32(v[h] >> 16);
+    }
+    s_xs[c * MR + r] = sum;
+  }
+  __syncthreads();
+
+  // 3. dot products, one 32-key piece per iteration, folded per quantisation group
+  const uint32_t magic = in_vgpr(E::kMagicPair);
+  float acc[MR];
+#pragma unroll
+  for (int r = 0; r < MR; ++r) acc[r] = 0.f;
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int c = (k0 + 128 * i) / 32 + pq;
+    u32x4 dq[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dq[j] = nibbles_to_operand(wv[i][j], magic);
+    const float zf = E::kMagic + (float)zi[i];
+    const float sci = decode_scale(sb[i], p.sdt);
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+      float gsum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const u32x4 xv = load16(s_x + (size_t)r * K + 32 * c + 8 * j);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) gsum = dot2_acc<T>(dq[j][h], xv[h], gsum);
+      }
+      acc[r] += sci * (gsum - zf * s_xs[c * MR + r]);
+      // finish this iteration's dot products here: left to itself the compiler
+      // unpacks every iteration's weights as they land and defers all dot products
+      // to the end, holding 8 x 16 unpacked registers (two workgroups per CU fewer)
+      asm volatile("" : "+v"(acc[r]));
+    }
+  }
+
+  // 4. the four lanes of a row, then the waves' slices in order
+#pragma unroll
+  for (int r = 0; r < MR; ++r) {
+    float v = acc[r];
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+    if (pq == 0) s_part[(wave * 16 + (lane >> 2)) * MR + r] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < 16 * MR) {
+    const int rr = threadIdx.x / MR, r = threadIdx.x - rr * MR;
+    float y = 0.f;
+    for (int w = 0; w < nw; ++w) y += s_part[(w * 16 + rr) * MR + r];
+    if (r < p.m && n0 + rr < p.n) ((T*)p.out)[(int64_t)r * p.o_stride + n0 + rr] = (T)y;
+  }
+}
+
 struct W4Plan {
   bool fast;
   bool wide;
   bool xlds;
+  int gemv;  // 1: the batch-1 GEMV kernel
   int mt, ns, bit, kw;
   int m_blocks, n_tiles;
   size_t lds;
@@ -398,6 +565,21 @@ W4Plan plan_w4a16(int64_t m, int64_t n, int64_t k, int g, bool act16) {
   pl.fast = act16 && k % 128 == 0 && g % 32 == 0 && k > 0 && n * k / 2 < ((int64_t)1 << 31);
   pl.wide = g % 128 == 0;
   if (!pl.fast) return pl;
+  // batch 1: the bandwidth GEMV when K splits into at most 8 wave slices of 1024
+  // keys (K <= 8192) or 2048 keys (K <= 16384) and the staged activation row fits
+  // the LDS budget. (A second activation row makes the compiler hoist every
+  // activation read and spill: m >= 2 takes the MFMA kernel.)
+  const int gemv_slice = k <= 8192 ? 1024 : 2048;
+  if (m == 1 && k % gemv_slice == 0 && k <= 16384) {
+    const int mr = 1;
+    const size_t lds = (size_t)mr * k * 2 + (size_t)(k / 32) * mr * 4 + (size_t)(k / gemv_slice) * 16 * mr * 4;
+    if (lds <= kLdsBudget) {
+      pl.gemv = mr;
+      pl.lds = lds;
+      pl.n_tiles = (int)((n + 15) / 16);
+      return pl;
+    }
+  }
   const size_t unit = pl.wide ? 128 : 32;
   const int64_t groups = k / g;
   const int iters = (int)(k / 128);
@@ -442,6 +624,15 @@ int launch_w4a16_x(const W4Params& p, const W4Plan& pl, hipStream_t stream) {
 
 template <typename T>
 int launch_w4a16_typed(const W4Params& p, const W4Plan& pl, hipStream_t stream) {
+  if (pl.gemv) {
+    if (p.k <= 8192)
+      hipLaunchKernelGGL((w4a16_gemv_kernel<T, 1, 8>), dim3((unsigned)pl.n_tiles),
+                         dim3((unsigned)(64 * (p.k / 1024))), pl.lds, stream, p);
+    else
+      hipLaunchKernelGGL((w4a16_gemv_kernel<T, 1, 16>), dim3((unsigned)pl.n_tiles),
+                         dim3((unsigned)(64 * (p.k / 2048))), pl.lds, stream, p);
+    return ss_host::launch_status("w4a16 gemv");
+  }
   if (pl.xlds) return launch_w4a16_x<T, 1, 1, 4, true>(p, pl, stream);
   if (pl.mt == 1) return launch_w4a16_x<T, 1, 4, 2, false>(p, pl, stream);
   if (pl.mt == 2) return launch_w4a16_x<T, 2, 2, 2, false>(p, pl, stream);

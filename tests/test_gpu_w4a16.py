@@ -87,6 +87,33 @@ def test_activation_paths(device, m, k, g):
     _assert_close(y, ref, f"m={m} k={k} g={g}")
 
 
+@pytest.mark.parametrize("n,k,g,act,sdt", [
+    (100, 1024, 128, torch.bfloat16, torch.float16),    # one wave; N not a multiple of 16
+    (48, 2048, 32, torch.float16, torch.bfloat16),      # four groups per 128 keys
+    (333, 4096, 64, torch.bfloat16, torch.float32),
+    (17, 8192, 128, torch.float16, torch.float16),      # 8 waves of 1024 keys
+    (64, 14336, 128, torch.bfloat16, torch.float16),    # 2048-key slices, 7 waves (the down projection)
+    (40, 16384, 64, torch.float16, torch.bfloat16),     # the largest K the GEMV takes
+])
+def test_batch1_gemv(device, n, k, g, act, sdt):
+    """M = 1 takes the bandwidth GEMV (one 1024-key wave slice per wave up to K = 8192,
+    2048-key slices up to 16384; four lanes per row): random zero points, every scale
+    dtype, ragged N."""
+    x, qw, s, z, ref = _host_case(n, k, 1, g, seed=n + k + g, act=act, sdt=sdt, zeros="random")
+    y = w4a16_gemm(x.to(device), qw.to(device), s.to(device), z.to(device), g)
+    assert y.shape == (1, n) and y.dtype == act
+    _assert_close(y, ref, f"gemv n={n} k={k} g={g}")
+
+
+def test_batch1_gemv_strided_activation(device):
+    """A strided single activation row (a view into a wider buffer) through the GEMV."""
+    x, qw, s, z, ref = _host_case(96, 4096, 1, 128, seed=77, zeros="random")
+    xd = torch.zeros((3, 8192), dtype=x.dtype, device=device)[1:2, 1024:5120]
+    xd.copy_(x.to(device))
+    y = w4a16_gemm(xd, qw.to(device), s.to(device), z.to(device), 128)
+    _assert_close(y, ref, "gemv strided x")
+
+
 def test_large_scale_table_takes_scalar_kernel(device):
     """k/group_size too large for the LDS scale table: the scalar kernel, same answer."""
     x, qw, s, z, ref = _host_case(32, 20480, 2, 32, seed=5, zeros="random")
