@@ -207,13 +207,37 @@ __global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
   WBlock wa, wb;
   if (it0 < it1) load_w(it0, wa);
 
-  // ---- prologue: scale table (+ activations) into LDS
-  for (int q = threadIdx.x; q < 16 * NS * p.groups; q += blockDim.x) {
-    const int r = q / p.groups, gi = q - r * p.groups;
-    const int64_t si = (int64_t)min(n0 + r, p.n - 1) * p.groups + gi;
-    const float sc = load_scale(p.sc, si, p.sdt);
-    s_sz[r * szrow + 2 * gi] = sc;
-    s_sz[r * szrow + 2 * gi + 1] = sc * (E::kMagic + (float)p.qz[si]);  // s * (MAGIC + z)
+  // ---- prologue: scale table (+ activations) into LDS. Eight entries per thread are
+  // requested before any is used (branch-free loads: a load inside a dtype branch
+  // makes the compiler wait for every outstanding load after it, which serialised
+  // the table behind one memory round trip per entry).
+  {
+    const int esize = p.sdt == SS_DTYPE_F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.sc, (uint32_t)((int64_t)p.n * p.groups * esize));
+    const __amdgpu_buffer_rsrc_t rzp = buffer_rsrc(p.qz, (uint32_t)((int64_t)p.n * p.groups * 4));
+    const int total = 16 * NS * p.groups;
+    for (int q0 = threadIdx.x; q0 < total; q0 += 8 * blockDim.x) {
+      uint32_t sbits[8];
+      int zv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int q = min(q0 + u * (int)blockDim.x, total - 1);
+        const int r = q / p.groups, gi = q - r * p.groups;
+        const int64_t si = (int64_t)min(n0 + r, p.n - 1) * p.groups + gi;
+        sbits[u] = scale_bits(rsc, si, esize);
+        zv[u] = __builtin_amdgcn_raw_buffer_load_b32(rzp, (int)(si * 4), 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int q = q0 + u * (int)blockDim.x;
+        if (q < total) {
+          const int r = q / p.groups, gi = q - r * p.groups;
+          const float sc = decode_scale(sbits[u], p.sdt);
+          s_sz[r * szrow + 2 * gi] = sc;
+          s_sz[r * szrow + 2 * gi + 1] = sc * (E::kMagic + (float)zv[u]);  // s * (MAGIC + z)
+        }
+      }
+    }
   }
   if (XLDS) {
     // rows [m0, m0 + rows) of x for all of K, permuted, plus their fold sums
@@ -239,11 +263,17 @@ __global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
   // Activation rows past M read row M-1 (a valid address); they only feed output
   // rows past M, which are never stored (each MFMA output row depends on its own
   // input row alone).
-  const T* xrow[MT];
-  int xl[MT];  // LDS row (XLDS)
+  // activation fragments by buffer loads: one uniform descriptor over this
+  // workgroup's rows and a 32-bit offset per lane (a 64-bit address per fragment
+  // costs register pairs, and their reuse made the loop head wait for the whole
+  // weight prefetch)
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(
+      (const T*)p.x + (int64_t)m0 * p.x_stride, (uint32_t)(((int64_t)(rows - 1) * p.x_stride + p.k) * sizeof(T)));
+  int xrow[MT];  // byte offset of this lane's activation row
+  int xl[MT];    // LDS row (XLDS)
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    xrow[mt] = (const T*)p.x + (int64_t)min(m0 + mt * 16 + ln, p.m - 1) * p.x_stride;
+    xrow[mt] = (int)((int64_t)min(mt * 16 + ln, rows - 1) * p.x_stride * (int64_t)sizeof(T));
     xl[mt] = min(mt * 16 + ln, rows - 1) * lrow;
   }
 
@@ -257,12 +287,17 @@ __global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
     if (XLDS) return;
 #pragma unroll
     for (int it = 0; it < BIT; ++it) {
-      const int kk = min(itb + it, it1 - 1) << 7;
+      // the iteration's key offset is uniform: it rides in the scalar offset, so the
+      // per-lane offsets stay loop-invariant (no vector register is redefined at the
+      // loop head, where reusing a register of the weight prefetch forces a full wait)
+      const int kk = (min(itb + it, it1 - 1) << 7) * (int)sizeof(T);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int koff = kk + (WIDE ? 32 * kg + 8 * s : 32 * s + 8 * kg);
+        const int klane = (WIDE ? 32 * kg + 8 * s : 32 * s + 8 * kg) * (int)sizeof(T);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) xb.x[XLDS ? 0 : mt][XLDS ? 0 : it][s] = load16(xrow[mt] + koff);
+        for (int mt = 0; mt < MT; ++mt)
+          xb.x[XLDS ? 0 : mt][XLDS ? 0 : it][s] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, xrow[mt] + klane, kk, 0));
       }
     }
   };
@@ -467,7 +502,7 @@ __global__ __launch_bounds__(512) void w4a16_gemv_kernel(const W4Params p) {
   u32x4 wv[IT];
 #pragma unroll
   for (int i = 0; i < IT; ++i)
-    wv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, vrow, 64 * i, kNonTemporal));
+    wv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, vrow, 64 * i, 0));
   const int esize = p.sdt == SS_DTYPE_F32 ? 4 : 2;
   const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.sc, (uint32_t)((int64_t)p.n * p.groups * esize));
   const __amdgpu_buffer_rsrc_t rzp = buffer_rsrc(p.qz, (uint32_t)((int64_t)p.n * p.groups * 4));
@@ -722,6 +757,8 @@ extern "C" int ss_w4a16_gemm(const void* x, void* out, const int32_t* qweight, c
   const bool act16 = act_dtype != SS_DTYPE_F32;
   ss::W4Plan pl = ss::plan_w4a16(m, n, k, group_size, act16);
   if (pl.fast && (!aligned16(x) || x_stride % 8 != 0 || !aligned16(qweight))) pl.fast = false;
+  // activation fragments are addressed by 32-bit byte offsets within a 64-row block
+  if (pl.fast && ((int64_t)63 * x_stride + k) * 2 >= ((int64_t)1 << 31)) pl.fast = false;
   hipStream_t s = (hipStream_t)stream;
   if (!pl.fast) {
     const int64_t total = m * n;
