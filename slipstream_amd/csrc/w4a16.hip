@@ -626,7 +626,14 @@ W4Plan plan_w4a16(int64_t m, int64_t n, int64_t k, int g, bool act16) {
   if (m <= 16 && x1 + sz1 <= kLdsBudget) {
     pl.mt = 1, pl.ns = 1, pl.bit = 4, pl.xlds = true;
   } else if (m <= 16) {
-    pl.mt = 1, pl.ns = 4, pl.bit = 2;  // 64 weight rows share each activation fragment
+    // 64 weight rows share each activation fragment, unless that leaves more than
+    // half the CUs idle: then 32 (twice the activation reads, twice the workgroups;
+    // measured faster for N = 4096 and 6144, slower for 14336)
+    const int64_t cus = ss_host::device_cu_count();
+    if ((n + 63) / 64 >= cus / 2)
+      pl.mt = 1, pl.ns = 4, pl.bit = 2;
+    else
+      pl.mt = 1, pl.ns = 2, pl.bit = 2;
   } else if (m <= 32) {
     pl.mt = 2, pl.ns = 2, pl.bit = 2;
   } else {
@@ -669,7 +676,8 @@ int launch_w4a16_typed(const W4Params& p, const W4Plan& pl, hipStream_t stream) 
     return ss_host::launch_status("w4a16 gemv");
   }
   if (pl.xlds) return launch_w4a16_x<T, 1, 1, 4, true>(p, pl, stream);
-  if (pl.mt == 1) return launch_w4a16_x<T, 1, 4, 2, false>(p, pl, stream);
+  if (pl.mt == 1 && pl.ns == 4) return launch_w4a16_x<T, 1, 4, 2, false>(p, pl, stream);
+  if (pl.mt == 1) return launch_w4a16_x<T, 1, 2, 2, false>(p, pl, stream);
   if (pl.mt == 2) return launch_w4a16_x<T, 2, 2, 2, false>(p, pl, stream);
   return launch_w4a16_x<T, 4, 2, 1, false>(p, pl, stream);
 }
