@@ -316,10 +316,16 @@ __device__ __forceinline__ i32x4 span_rsrc(const char* base, int bytes) {
 // so that the compiler, which cannot tell the pipeline stages apart, adds no
 // vmcnt waits of its own before LDS reads: the kernel waits with explicit
 // vmcnt counts and a barrier before a stage is read.
+// The compiler's hazard recognizer does not look inside the asm, so the asm
+// keeps the wait states itself: the descriptor's size is often written by a
+// VALU instruction (v_readfirstlane), and a VMEM instruction may read an SGPR a
+// VALU instruction wrote only 5 wait states later (one for M0). With fewer, the
+// load can take the previous descriptor's size: after an absent block (size 0)
+// the first rows of the next group would read as zeros.
 __device__ __forceinline__ void dma16(i32x4 rsrc, LdsBytes lds, int voff) {
   const uint32_t m0 = (uint32_t)(uintptr_t)lds;
   asm volatile(
-      "s_nop 0\n\t"
+      "s_nop 4\n\t"
       "buffer_load_dwordx4 %0, %1, 0 offen lds"
       :
       : "v"(voff), "s"(rsrc), "{m0}"(m0)

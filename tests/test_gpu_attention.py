@@ -308,6 +308,35 @@ def test_prefill_table_holes(device):
     assert_attn_close(out, ref, "prefill holes")
 
 
+@pytest.mark.parametrize("ctx,holes", [((700, 200), ()), ((520, 333), ((0, 3), (1, 2)))])
+def test_prefill_every_key_weighted(device, ctx, holes):
+    """K = 0 makes every visible key's weight 1/(visible keys); V one-hot on key // 8 then
+    reads each 8-key bucket's share in one output column, so a key that is lost, zeroed or
+    counted twice shows up in its own column. Covers the last (partial) tile of every
+    chunk and, with holes, the block after an absent one in the same 16-key group."""
+    b = workloads.build_batch(list(ctx), [8] * len(ctx), n_q=32, n_kv=8, head_dim=128, block_size=16,
+                              dtype=torch.bfloat16, device="cpu", seed=sum(ctx))
+    kv = b.kv_cache
+    kv[0, 0].zero_()
+    kv[0, 1].zero_()
+    for s, c in enumerate(ctx):
+        for p in range(c):
+            kv[0, 1, b.tables_host[s][p // 16], p % 16, :, (p // 8) % 128] = 1.0
+    tables = [list(t) for t in b.tables_host]
+    for s, blk in holes:
+        tables[s][blk] = -1
+    width = b.block_tables.shape[1]
+    bt = torch.full((len(ctx), width), -1, dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, : len(t)] = torch.tensor(t, dtype=torch.int32)
+    b.block_tables = bt
+    ref = ora.paged_attention(f64(b.padded_q()), f64(kv), tables_array(tables, width), np.array(b.ctx_host), 0,
+                              b.scale, 16)
+    _to(b, device)
+    out = paged_attention_prefill(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
+    assert_attn_close(out, ref, f"prefill bucket weights ctx={ctx} holes={holes}")
+
+
 def test_prefill_head_dim_256(device):
     b = workloads.build_batch([40, 300], [40, 40], n_q=8, n_kv=2, head_dim=256, block_size=16,
                               dtype=torch.bfloat16, device="cpu", seed=256)
