@@ -135,11 +135,16 @@ int ss_paged_attention_varlen(const void* q, void* out, const void* k_cache, con
  * quant_ref.py:38-42). bf16/fp16 activations with k % 128 == 0 and
  * group_size % 32 == 0 (16-byte aligned x rows and qweight, n*k/2 < 2^31, and
  * a per-workgroup scale table of 16 * (2*k/group_size + 2) floats within 64 KiB
- * of LDS: k/group_size <= 480 for m <= 16) take the MFMA kernel; everything
- * else a scalar fp32 kernel. The result does not depend on timing (no
- * cross-workgroup reduction).
- * workspace: ss_w4a16_workspace_size() reports 0 bytes; the arguments are kept
- * so a later kernel may use scratch without an ABI change (pass NULL, 0).
+ * of LDS: k/group_size <= 480 for m <= 16) take the MFMA kernels (m = 1: a
+ * bandwidth GEMV; m >= 2 with group_size % 128 == 0: a tiled kernel that may
+ * split K over workgroups); everything else a scalar fp32 kernel. The result
+ * does not depend on timing: split-K partials are added in a fixed order by a
+ * second kernel, never by atomics.
+ * workspace: ss_w4a16_workspace_size() reports the bytes of the split-K
+ * partials (ranges * m * n floats; 0 when the plan does not split). Pass at
+ * least that many bytes, 16-byte aligned; with less (or NULL, 0) the call still
+ * succeeds on the untiled MFMA kernel, which needs no scratch. Calls that share
+ * one workspace must be ordered on one stream.
  */
 int ss_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int group_size, int act_dtype,
                             int64_t* bytes);

@@ -16,11 +16,17 @@
 // (k0,k4),(k1,k5),(k2,k6),(k3,k7) of each word, and every activation fragment is
 // permuted the same way in registers (v_perm_b32), so the dot products pair up.
 //
-// Work split: a workgroup owns 16*NS weight rows and 16*MT activation rows; its
-// KW waves split K into contiguous slices (each wave streams its own slice of
-// the rows: coalesced 16-byte loads, the next block in flight while the current
-// one computes), and one LDS pass adds the slices in wave order. There is no
-// synchronisation between workgroups, so the result does not depend on timing.
+// Untiled kernel (w4a16_kernel): a workgroup owns 16*NS weight rows and 16*MT
+// activation rows; its KW waves split K into contiguous slices (each wave streams
+// its own slice of the rows: coalesced 16-byte loads, the next block in flight
+// while the current one computes), and one LDS pass adds the slices in wave
+// order. There is no synchronisation between workgroups.
+//
+// Tiled kernel (w4a16_tile_kernel, m >= 2 and g % 128 == 0; m <= 16 only for
+// K >= 8192): four waves split 64*NS weight rows and share the activation tile
+// through LDS; K is split over workgroups and a second kernel adds the fp32
+// partials in range order. Batch 1 takes a bandwidth GEMV. In every case the
+// result does not depend on timing.
 //
 // Generic path (any other shape, fp32 activations): one thread per output,
 // fp32 dequant and dot product.
@@ -83,6 +89,29 @@ __device__ __forceinline__ float decode_scale(uint32_t bits, int sdt) {
   const float f16 = (float)__builtin_bit_cast(f16_t, (uint16_t)(bits & 0xFFFFu));
   const float b16 = __builtin_bit_cast(float, bits << 16);
   return sdt == SS_DTYPE_F16 ? f16 : (sdt == SS_DTYPE_BF16 ? b16 : __builtin_bit_cast(float, bits));
+}
+
+// decode_scale without a branch on the dtype (the branches split the loop body into
+// blocks, and the compiler then sinks whole folds past them, keeping every stage's
+// MFMA partial sums live): all three decodings, merged under uniform bit masks
+// (f16_mask / bf16_mask all-ones for that dtype, else zero).
+__device__ __forceinline__ float decode_scale_masked(uint32_t bits, uint32_t f16_mask, uint32_t bf16_mask) {
+  const uint32_t f16 = __builtin_bit_cast(uint32_t, (float)__builtin_bit_cast(f16_t, (uint16_t)(bits & 0xFFFFu)));
+  const uint32_t b16 = bits << 16;
+  return __builtin_bit_cast(float, (f16 & f16_mask) | (b16 & bf16_mask) | (bits & ~(f16_mask | bf16_mask)));
+}
+
+// Sum over the 16 lanes of a DPP row (every lane of the row gets the total).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f32<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_f32<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_f32<0x141>(x);  // row_half_mirror
+  x += dpp_f32<0x140>(x);  // row_mirror
+  return x;
 }
 
 // A constant held in a VGPR. gfx9 VOP3 instructions take no literal and read at most
@@ -419,6 +448,266 @@ __global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
     }
 }
 
+// Tiled W4A16 GEMM (m >= 2, g % 128 == 0): the activation tile is shared by the
+// workgroup through LDS, so each activation element is read from memory once per
+// 64*NS weight rows (the kernel above reads it once per 16*NS rows, which made
+// activation traffic several times the weight traffic for m >= 16).
+//
+// A workgroup owns 16*MT activation rows and 64*NS weight rows (four waves of
+// 16*NS rows each, every wave against all 16*MT activation rows) over one range of
+// `kchunk` 128-key stages (blockIdx.z). With several ranges (split K) each writes
+// fp32 partials part[z][m][n] and w4a16_splitk_reduce_kernel adds them in range
+// order, so the result does not depend on timing.
+//   - Once per workgroup: the scale table of its rows and range, as pairs
+//     (s, s * (MAGIC + z)) in LDS (dynamic shared memory). Per-stage scale loads
+//     from memory, 16 scattered words per instruction, took the memory pipeline
+//     slots the weight stream needs.
+//   - Per stage: the activation stage (16*MT rows x 128 keys) goes through
+//     registers into LDS (double buffered), permuted to the nibble order, with each
+//     row's sum over the stage (the X term of the fold; g % 128 == 0 puts a stage
+//     in one quantisation group). Weights stream straight into registers PF
+//     stages ahead: one 16-byte load per lane and 16-row tile, four lanes reading a
+//     row's 64 contiguous bytes. Prefetches past the range use an offset past the
+//     end of the buffer: they return zeros without touching memory, and the loop
+//     needs no branch.
+//   - Per 32-key step the MFMA accumulates G = sum x (MAGIC + q) for every
+//     (activation tile, weight tile) pair; one fold per stage:
+//       acc += s * G - s * (MAGIC + z) * X.
+// Every range is a whole number of PF stages (host-checked).
+constexpr int kOutOfRange = 0x40000000;  // buffer offset past any operand (< 2^31 bytes)
+
+template <typename T, int MT, int NS, int PF>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void w4a16_tile_kernel(
+    const W4Params p, float* __restrict__ part, int kchunk) {
+  typedef W4Elem<T> E;
+  constexpr int BM = 16 * MT;
+  constexpr int LROW = 128 + 8;  // LDS row of an activation stage, elements (16-byte skew)
+  __shared__ __attribute__((aligned(16))) T s_x[2][BM][LROW];
+  __shared__ __attribute__((aligned(16))) float s_sum[2][BM];
+  extern __shared__ __attribute__((aligned(16))) char s_dyn[];
+  float2* const s_sz = (float2*)s_dyn;  // [64*NS rows][gr + 1] (s, s*(MAGIC+z))
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ln = lane & 15, kg = lane >> 4;
+  // grid (K ranges, weight tiles, activation tiles): the ranges of one tile are
+  // dispatched together, so the resident workgroups read whole weight rows
+  // (adjacent ranges) rather than one range of every row
+  const int zr = blockIdx.x;
+  const int nb = blockIdx.y * 64 * NS;  // the workgroup's first weight row
+  const int n0 = nb + wave * 16 * NS;   // this wave's
+  const int m0 = blockIdx.z * BM;
+  const int rows = min(BM, p.m - m0);
+  const int i0 = zr * kchunk;
+  const int i1 = min(p.k >> 7, i0 + kchunk);
+  const int g0 = (i0 << 7) / p.g;                     // first group of the range
+  const int gr = (((i1 << 7) - 1) / p.g) - g0 + 1;    // groups in the range
+  const int srow = gr + 1;                            // LDS row of the table (skewed)
+  const uint32_t magic = in_vgpr(E::kMagicPair);
+
+  // ---- scale table of rows [nb, nb + 64*NS) x groups [g0, g0 + gr), TB entries per
+  // thread per batch. The first batch is requested before the weight prologue and
+  // stored after it, so the weights do not wait for a table round trip.
+  constexpr int TB = 8;
+  const int esize = p.sdt == SS_DTYPE_F32 ? 4 : 2;
+  const uint32_t f16_mask = p.sdt == SS_DTYPE_F16 ? ~0u : 0u, bf16_mask = p.sdt == SS_DTYPE_BF16 ? ~0u : 0u;
+  const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.sc, (uint32_t)((int64_t)p.n * p.groups * esize));
+  const __amdgpu_buffer_rsrc_t rzp = buffer_rsrc(p.qz, (uint32_t)((int64_t)p.n * p.groups * 4));
+  const int total = 64 * NS * gr;
+  uint32_t sbits[TB];
+  int zv[TB];
+  auto table_load = [&](int q0) {
+#pragma unroll
+    for (int u = 0; u < TB; ++u) {
+      const int q = min(q0 + 256 * u, total - 1);
+      const int r = q / gr, gl = q - r * gr;
+      const int si = min(nb + r, p.n - 1) * p.groups + g0 + gl;
+      sbits[u] = scale_bits(rsc, si, esize);
+      zv[u] = __builtin_amdgcn_raw_buffer_load_b32(rzp, si * 4, 0, 0);
+    }
+  };
+  auto table_store = [&](int q0) {
+#pragma unroll
+    for (int u = 0; u < TB; ++u) {
+      const int q = q0 + 256 * u;
+      if (q < total) {
+        const int r = q / gr, gl = q - r * gr;
+        const float sc = decode_scale_masked(sbits[u], f16_mask, bf16_mask);
+        s_sz[r * srow + gl] = float2{sc, sc * (E::kMagic + (float)zv[u])};
+      }
+    }
+  };
+  table_load(threadIdx.x);
+
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(p.qw, (uint32_t)((int64_t)p.n * p.k / 2));
+  int w_off[NS], t_row[NS];
+#pragma unroll
+  for (int ns = 0; ns < NS; ++ns) {
+    const int r = min(n0 + ns * 16 + ln, p.n - 1);  // rows past N repeat row N-1; never stored
+    w_off[ns] = r * (p.k / 2) + 16 * kg;
+    t_row[ns] = (wave * 16 * NS + ns * 16 + ln) * srow;
+  }
+  auto load_w = [&](int i, u32x4 (&w)[NS]) {
+    const int so = i < i1 ? i * 64 : kOutOfRange;
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns)
+      w[ns] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, w_off[ns], so, kNonTemporal));
+  };
+
+  // activation staging: chunk q = threadIdx.x + 256 u is row q / 16, keys 8 (q % 16)..+7
+  // of the stage; rows past M read row M-1 (their outputs are never stored)
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(
+      (const T*)p.x + (int64_t)m0 * p.x_stride, (uint32_t)(((int64_t)(rows - 1) * p.x_stride + p.k) * sizeof(T)));
+  int x_off[MT];
+#pragma unroll
+  for (int u = 0; u < MT; ++u) {
+    const int q = threadIdx.x + 256 * u;
+    x_off[u] = (int)(((int64_t)min(q >> 4, rows - 1) * p.x_stride + 8 * (q & 15)) * (int64_t)sizeof(T));
+  }
+  u32x4 xr[MT];
+  auto load_x = [&](int i) {
+    const int so = i < i1 ? i * 128 * (int)sizeof(T) : kOutOfRange;
+#pragma unroll
+    for (int u = 0; u < MT; ++u)
+      xr[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, x_off[u], so, 0));
+  };
+  auto stage_x = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < MT; ++u) {
+      const int q = threadIdx.x + 256 * u;
+      const int r = q >> 4, c = q & 15;
+      float sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sum += E::to_f32(xr[u][j] & 0xFFFFu) + E::to_f32(xr[u][j] >> 16);
+      sum = row16_sum(sum);  // the 16 chunks of row r sit in one DPP row
+      store16(&s_x[buf][r][8 * c], permute_x(xr[u]));
+      // every lane of the row stores the same total: no branch, so the loop body stays
+      // one block (a block boundary lets the compiler sink the folds to the loop end,
+      // keeping every stage's partial sums live)
+      s_sum[buf][r] = sum;
+    }
+  };
+
+  f32x4 acc[MT][NS];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) acc[mt][ns] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int i, int buf, const u32x4 (&w)[NS]) {
+    f32x4 G[MT][NS];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u32x4 a[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) a[mt] = *reinterpret_cast<const u32x4*>(&s_x[buf][mt * 16 + ln][8 * (4 * kg + s)]);
+#pragma unroll
+      for (int ns = 0; ns < NS; ++ns) {
+        const u32x4 b = nibbles_to_operand(w[ns][s], magic);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) G[mt][ns] = Elem<T>::mfma(a[mt], b, s == 0 ? zero4 : G[mt][ns]);
+      }
+    }
+    f32x4 X[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) X[mt] = *reinterpret_cast<const f32x4*>(&s_sum[buf][mt * 16 + 4 * kg]);
+    const int gl = ((i << 7) / p.g) - g0;
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) {
+      const float2 sz = s_sz[t_row[ns] + gl];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[mt][ns][e] = fmaf(sz.x, G[mt][ns][e], fmaf(-sz.y, X[mt][e], acc[mt][ns][e]));
+    }
+  };
+
+  u32x4 ring[PF][NS];
+#pragma unroll
+  for (int u = 0; u < PF; ++u) load_w(i0 + u, ring[u]);
+  load_x(i0);
+  table_store(threadIdx.x);
+  for (int q0 = threadIdx.x + TB * 256; q0 < total; q0 += TB * 256) {  // large tables only
+    table_load(q0);
+    table_store(q0);
+  }
+  stage_x(0);
+  __syncthreads();  // the scale table and the first activation stage
+  for (int i = i0; i < i1; i += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int buf = (i - i0 + u) & 1;
+      load_x(i + u + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(i + u, buf, ring[u]);
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(i + u + PF, ring[u]);
+      __builtin_amdgcn_sched_barrier(0);
+      stage_x(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // lane holds C[m0 + mt*16 + 4kg + e][n0 + ns*16 + ln]
+  const bool split = gridDim.x > 1;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) {
+      const int n = n0 + ns * 16 + ln;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + mt * 16 + 4 * kg + e;
+        if (m < p.m && n < p.n) {
+          if (split)
+            part[((int64_t)zr * p.m + m) * p.n + n] = acc[mt][ns][e];
+          else
+            ((T*)p.out)[(int64_t)m * p.o_stride + n] = (T)acc[mt][ns][e];
+        }
+      }
+    }
+}
+
+// out[m][n] = sum over ranges z (in order) of part[z][m][n]; VEC consecutive n per thread.
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void w4a16_splitk_reduce_kernel(const float* __restrict__ part, void* out, int m,
+                                                                  int n, int splits, int64_t o_stride) {
+  const int64_t per_row = n / VEC;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)m * per_row) return;
+  const int r = (int)(idx / per_row);
+  const int c = (int)(idx - (int64_t)r * per_row) * VEC;
+  const int64_t plane = (int64_t)m * n;
+  const float* src = part + (int64_t)r * n + c;
+  float s[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) s[v] = 0.f;
+  // eight ranges' loads in flight at a time, added in range order
+  for (int z0 = 0; z0 < splits; z0 += 8) {
+    float t[8][VEC];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int z = min(z0 + j, splits - 1);
+      if (VEC == 4) {
+        const f32x4 v4 = *reinterpret_cast<const f32x4*>(src + z * plane);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) t[j][v] = v4[v];
+      } else {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) t[j][v] = src[z * plane + v];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) s[v] += z0 + j < splits ? t[j][v] : 0.f;
+  }
+  T* dst = (T*)out + (int64_t)r * o_stride + c;
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) dst[v] = (T)s[v];
+}
+
 template <typename T>
 __device__ __forceinline__ float elem_to_f32(T v) {
   return (float)v;
@@ -588,14 +877,73 @@ struct W4Plan {
   bool wide;
   bool xlds;
   int gemv;  // 1: the batch-1 GEMV kernel
-  int mt, ns, bit, kw;
+  bool tile;  // the tiled kernel (activations shared through LDS)
+  int mt, ns, bit, kw, pf;
   int m_blocks, n_tiles;
+  int ks, kchunk;  // tiled kernel: K ranges and 128-key stages per range
   size_t lds;
 };
 
+// Tiled kernel for m >= 2 when g % 128 == 0 and K is a whole number of PF-stage
+// rounds. Shapes (activation tiles MT, weight tiles NS per wave, prefetch depth PF)
+// by m: the bandwidth-bound sizes keep eight stages of weights in flight per wave;
+// m > 64 (MFMA-bound) takes 64 x 64 wave tiles. The K split aims at two
+// workgroups per CU (one for m > 64), each range at least one round of PF stages,
+// with the workgroup's scale table within kTileTableMax bytes of LDS; the
+// partials take ks * m * n floats of workspace.
+constexpr int kTileTableMax = 64 * 1024;
+
+size_t tile_table_bytes(int ns, int kchunk, int g) {
+  const int gr = (kchunk * 128 + g - 1) / g + 1;  // groups a range can touch
+  return (size_t)64 * ns * (gr + 1) * 8;
+}
+
+bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
+  if (!pl.wide || m < 2) return false;
+  // m <= 16 is weight-bandwidth bound and the untiled kernel shares activations
+  // well enough there; for K < 8192 it measured faster (no reduction launch)
+  if (m <= 16 && k < 8192) return false;
+  int mt, ns, pf;
+  if (m <= 16)
+    mt = 1, ns = 2, pf = 8;
+  else if (m <= 32)
+    mt = 2, ns = 2, pf = 8;
+  else if (m <= 64)
+    mt = 4, ns = 2, pf = 4;
+  else
+    mt = 4, ns = 4, pf = 2;
+  const int64_t iters = k / 128;
+  if (iters % pf) return false;
+  const int64_t n_tiles = (n + 64 * ns - 1) / (64 * ns);
+  const int64_t m_blocks = (m + 16 * mt - 1) / (16 * mt);
+  if (n_tiles > 65535 || m_blocks > 65535) return false;
+  const int64_t target = (m <= 64 ? 2LL : 1LL) * ss_host::device_cu_count();
+  const int64_t tiles = n_tiles * m_blocks;
+  const int64_t rounds = iters / pf;
+  int64_t ks = (target + tiles - 1) / tiles;
+  ks = ks < 1 ? 1 : (ks > rounds ? rounds : ks);
+  if (ks > 65535) return false;
+  int64_t per = (rounds + ks - 1) / ks;
+  while (per > 1 && tile_table_bytes(ns, (int)(per * pf), g) > (size_t)kTileTableMax) --per;
+  if (tile_table_bytes(ns, (int)(per * pf), g) > (size_t)kTileTableMax) return false;
+  pl.tile = true;
+  pl.mt = mt, pl.ns = ns, pl.pf = pf;
+  pl.n_tiles = (int)n_tiles;
+  pl.m_blocks = (int)m_blocks;
+  pl.kchunk = (int)(per * pf);
+  pl.ks = (int)((rounds + per - 1) / per);
+  if (pl.ks > 65535) return false;
+  pl.lds = tile_table_bytes(ns, pl.kchunk, g);
+  return true;
+}
+
+int64_t tile_workspace_bytes(const W4Plan& pl, int64_t m, int64_t n) {
+  return pl.tile && pl.ks > 1 ? (int64_t)pl.ks * m * n * 4 : 0;
+}
+
 constexpr size_t kLdsBudget = 64 * 1024;  // LDS bytes per workgroup
 
-W4Plan plan_w4a16(int64_t m, int64_t n, int64_t k, int g, bool act16) {
+W4Plan plan_w4a16(int64_t m, int64_t n, int64_t k, int g, bool act16, bool allow_tile = true) {
   W4Plan pl = {};
   pl.fast = act16 && k % 128 == 0 && g % 32 == 0 && k > 0 && n * k / 2 < ((int64_t)1 << 31);
   pl.wide = g % 128 == 0;
@@ -615,6 +963,8 @@ W4Plan plan_w4a16(int64_t m, int64_t n, int64_t k, int g, bool act16) {
       return pl;
     }
   }
+  if (allow_tile && plan_tile(pl, m, n, k, g)) return pl;
+  pl.tile = false;
   const size_t unit = pl.wide ? 128 : 32;
   const int64_t groups = k / g;
   const int iters = (int)(k / 128);
@@ -664,8 +1014,41 @@ int launch_w4a16_x(const W4Params& p, const W4Plan& pl, hipStream_t stream) {
   return ss_host::launch_status("w4a16 gemm");
 }
 
+template <typename T, int MT, int NS, int PF>
+int launch_w4a16_tile(const W4Params& p, const W4Plan& pl, float* part, hipStream_t stream) {
+  static bool attr_set = false;  // per instantiation; the attribute is process-wide
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)w4a16_tile_kernel<T, MT, NS, PF>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            kTileTableMax) != hipSuccess) {
+      ss_host::set_error("w4a16 gemm: cannot reserve %d bytes of LDS", kTileTableMax);
+      return SS_ERR_UNSUPPORTED;
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((w4a16_tile_kernel<T, MT, NS, PF>), dim3((unsigned)pl.ks, (unsigned)pl.n_tiles, (unsigned)pl.m_blocks),
+                     dim3(256), pl.lds, stream, p, part, pl.kchunk);
+  int st = ss_host::launch_status("w4a16 gemm (tiled)");
+  if (st != SS_OK || pl.ks == 1) return st;
+  const bool vec = p.n % 4 == 0;
+  const int64_t threads = (int64_t)p.m * (vec ? p.n / 4 : p.n);
+  const unsigned blocks = (unsigned)((threads + 255) / 256);
+  if (vec)
+    hipLaunchKernelGGL((w4a16_splitk_reduce_kernel<T, 4>), dim3(blocks), dim3(256), 0, stream, part, p.out, p.m, p.n,
+                       pl.ks, p.o_stride);
+  else
+    hipLaunchKernelGGL((w4a16_splitk_reduce_kernel<T, 1>), dim3(blocks), dim3(256), 0, stream, part, p.out, p.m, p.n,
+                       pl.ks, p.o_stride);
+  return ss_host::launch_status("w4a16 split-K reduce");
+}
+
 template <typename T>
-int launch_w4a16_typed(const W4Params& p, const W4Plan& pl, hipStream_t stream) {
+int launch_w4a16_typed(const W4Params& p, const W4Plan& pl, float* part, hipStream_t stream) {
+  if (pl.tile) {
+    if (pl.mt == 1) return launch_w4a16_tile<T, 1, 2, 8>(p, pl, part, stream);
+    if (pl.mt == 2) return launch_w4a16_tile<T, 2, 2, 8>(p, pl, part, stream);
+    if (pl.ns == 2) return launch_w4a16_tile<T, 4, 2, 4>(p, pl, part, stream);
+    return launch_w4a16_tile<T, 4, 4, 2>(p, pl, part, stream);
+  }
   if (pl.gemv) {
     if (p.k <= 8192)
       hipLaunchKernelGGL((w4a16_gemv_kernel<T, 1, 8>), dim3((unsigned)pl.n_tiles),
@@ -725,7 +1108,8 @@ extern "C" int ss_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int grou
     ss_host::set_error("w4a16 workspace: null output pointer");
     return SS_ERR_INVALID;
   }
-  *bytes = 0;  // the kernels need no scratch
+  const ss::W4Plan pl = ss::plan_w4a16(m, n, k, group_size, act_dtype != SS_DTYPE_F32);
+  *bytes = pl.fast ? ss::tile_workspace_bytes(pl, m, n) : 0;
   return SS_OK;
 }
 
@@ -733,8 +1117,6 @@ extern "C" int ss_w4a16_gemm(const void* x, void* out, const int32_t* qweight, c
                              const int32_t* qzeros, int64_t m, int64_t n, int64_t k, int group_size,
                              int64_t x_stride, int64_t o_stride, int act_dtype, int scale_dtype,
                              void* workspace, int64_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   const char* who = "w4a16 gemm";
   int st = check_w4a16(who, m, n, k, group_size, act_dtype, scale_dtype);
   if (st != SS_OK) return st;
@@ -767,6 +1149,18 @@ extern "C" int ss_w4a16_gemm(const void* x, void* out, const int32_t* qweight, c
   if (pl.fast && (!aligned16(x) || x_stride % 8 != 0 || !aligned16(qweight))) pl.fast = false;
   // activation fragments are addressed by 32-bit byte offsets within a 64-row block
   if (pl.fast && ((int64_t)63 * x_stride + k) * 2 >= ((int64_t)1 << 31)) pl.fast = false;
+  // scale and zero-point offsets are 32-bit byte offsets
+  if (pl.fast && n * (k / group_size) * 4 >= ((int64_t)1 << 31)) pl.fast = false;
+  if (pl.fast && pl.tile && pl.ks > 1) {
+    // the K split needs the workspace ss_w4a16_workspace_size reports; without it
+    // (or unaligned) the untiled MFMA kernel runs, which needs none
+    const int64_t need = ss::tile_workspace_bytes(pl, m, n);
+    if (!workspace || workspace_bytes < need || !aligned16(workspace)) {
+      const bool fast = pl.fast;
+      pl = ss::plan_w4a16(m, n, k, group_size, act16, false);
+      pl.fast = pl.fast && fast;
+    }
+  }
   hipStream_t s = (hipStream_t)stream;
   if (!pl.fast) {
     const int64_t total = m * n;
@@ -788,6 +1182,7 @@ extern "C" int ss_w4a16_gemm(const void* x, void* out, const int32_t* qweight, c
     return SS_ERR_UNSUPPORTED;
   }
   p.kw = pl.kw;
-  if (act_dtype == SS_DTYPE_BF16) return ss::launch_w4a16_typed<ss::bf16_t>(p, pl, s);
-  return ss::launch_w4a16_typed<ss::f16_t>(p, pl, s);
+  float* part = (float*)workspace;
+  if (act_dtype == SS_DTYPE_BF16) return ss::launch_w4a16_typed<ss::bf16_t>(p, pl, part, s);
+  return ss::launch_w4a16_typed<ss::f16_t>(p, pl, part, s);
 }

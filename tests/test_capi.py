@@ -78,7 +78,12 @@ def test_w4a16_argument_errors_need_no_device():
     assert b"multiple of 8" in lib.ss_last_error()
     assert lib.ss_w4a16_workspace_size(4, 64, 100, 32, _ffi.SS_DTYPE_BF16, ctypes.byref(out)) == _ffi.SS_ERR_INVALID
     assert lib.ss_w4a16_workspace_size(1, 4096, 4096, 128, _ffi.SS_DTYPE_BF16, ctypes.byref(out)) == _ffi.SS_OK
-    assert out.value >= 0
+    assert out.value == 0  # batch 1: the GEMV, no scratch
+    # the tiled kernel splits K over workgroups: fp32 partials [ranges][m][n]
+    assert lib.ss_w4a16_workspace_size(64, 4096, 14336, 128, _ffi.SS_DTYPE_BF16, ctypes.byref(out)) == _ffi.SS_OK
+    assert out.value > 0 and out.value % (64 * 4096 * 4) == 0
+    assert lib.ss_w4a16_workspace_size(64, 4096, 14336, 128, _ffi.SS_DTYPE_F32, ctypes.byref(out)) == _ffi.SS_OK
+    assert out.value == 0  # fp32 activations take the scalar kernel
     st = lib.ss_w4a16_gemm(None, None, None, None, None, 0, 8, 256, 128, 256, 8, _ffi.SS_DTYPE_BF16,
                            _ffi.SS_DTYPE_F16, None, 0, None)
     assert st == _ffi.SS_OK  # empty batch touches nothing

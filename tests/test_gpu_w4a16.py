@@ -114,6 +114,46 @@ def test_batch1_gemv_strided_activation(device):
     _assert_close(y, ref, "gemv strided x")
 
 
+@pytest.mark.parametrize("m,k,n,g,act,sdt", [
+    (50, 3584, 12750, 128, torch.bfloat16, torch.float16),   # 4 K ranges of 8, 8, 8, 4 stages; ragged M, N
+    (33, 3584, 2000, 896, torch.float16, torch.bfloat16),    # groups of 7 stages straddle the ranges
+    (100, 4096, 1000, 256, torch.bfloat16, torch.float32),   # 64x64 wave tiles, a partial second M block
+    (24, 8192, 3000, 512, torch.float16, torch.float16),     # 32-row activation tiles
+    (9, 8192, 700, 128, torch.bfloat16, torch.bfloat16),     # m <= 16 at K >= 8192 takes the tiled kernel
+])
+def test_tiled_split_k(device, m, k, n, g, act, sdt):
+    """The tiled kernel (activations shared through LDS, K split over workgroups with
+    fp32 partials added in range order): uneven ranges, groups straddling ranges,
+    ragged M and N, every scale dtype."""
+    x, qw, s, z, ref = _host_case(n, k, m, g, seed=m + k + n, act=act, sdt=sdt, zeros="random")
+    xd, qd, sd, zd = x.to(device), qw.to(device), s.to(device), z.to(device)
+    y = w4a16_gemm(xd, qd, sd, zd, g)
+    _assert_close(y, ref, f"tiled m={m} k={k} n={n} g={g}")
+    assert torch.equal(y, w4a16_gemm(xd, qd, sd, zd, g))  # repeat: bit-identical
+
+
+def test_tiled_without_workspace_takes_untiled_kernel(device):
+    """Through the C-ABI with no workspace, a shape planned for the K split runs the
+    untiled MFMA kernel instead: same answer within the tolerance."""
+    import ctypes
+    from slipstream_amd import _ffi
+
+    m, k, n, g = 64, 4096, 2048, 128
+    x, qw, s, z, ref = _host_case(n, k, m, g, seed=64, zeros="random")
+    xd, qd, sd, zd = x.to(device), qw.to(device), s.to(device), z.to(device)
+    lib = _ffi.lib()
+    need = ctypes.c_int64(0)
+    assert lib.ss_w4a16_workspace_size(m, n, k, g, _ffi.SS_DTYPE_BF16, ctypes.byref(need)) == _ffi.SS_OK
+    assert need.value > 0
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+    st = lib.ss_w4a16_gemm(xd.data_ptr(), out.data_ptr(), qd.data_ptr(), sd.data_ptr(), zd.data_ptr(), m, n, k, g,
+                           k, n, _ffi.SS_DTYPE_BF16, _ffi.SS_DTYPE_F16, None, 0, _ffi.stream_ptr(xd.device))
+    assert st == _ffi.SS_OK, lib.ss_last_error()
+    torch.cuda.synchronize()
+    _assert_close(out, ref, "no workspace")
+    _assert_close(w4a16_gemm(xd, qd, sd, zd, g), ref, "with workspace")
+
+
 def test_large_scale_table_takes_scalar_kernel(device):
     """k/group_size too large for the LDS scale table: the scalar kernel, same answer."""
     x, qw, s, z, ref = _host_case(32, 20480, 2, 32, seed=5, zeros="random")
