@@ -42,9 +42,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the host-side reference timing")
     ap.add_argument("--skip-extra", action="store_true", help="headline only (no packed / prefix lines)")
-    ap.add_argument("--only", choices=["all", "w4a16", "copy"], default="all",
-                    help="w4a16: run the C5 section alone; copy: 1 GiB device copies of known size, the "
-                         "calibration kernel for the FETCH_SIZE/WRITE_SIZE counters (profiling aids)")
+    ap.add_argument("--only", choices=["all", "w4a16", "block_copy", "copy"], default="all",
+                    help="w4a16 / block_copy: run that section alone; copy: 1 GiB device copies of known "
+                         "size, the calibration kernel for the FETCH_SIZE/WRITE_SIZE counters (profiling aids)")
     return ap.parse_args()
 
 
@@ -251,6 +251,44 @@ def w4a16_section(dev, steps: int, warmup: int) -> dict:
             "cases": cases, "layer_us_by_m": {str(m): round(v, 2) for m, v in layer_us.items()}}
 
 
+def block_copy_section(dev, steps: int, warmup: int) -> dict:
+    """Page copies: copy-on-write of 2048 random pages of the C2 pool
+    (one layer: K and V planes, 32 KB pages) and swap out / in of 512 pages to a pinned
+    host cache. Bytes: every copied page is read once and written once."""
+    import numpy as np
+    import torch
+
+    from slipstream_amd import workloads
+    from slipstream_amd.kernels import copy_blocks, swap_blocks
+
+    b = workloads.llama_decode(device=dev, seed=1)
+    kv = b.kv_cache
+    nb = kv.shape[2]
+    page = kv[0, 0, 0].numel() * kv.element_size()
+    rng = np.random.default_rng(0)
+    blocks = rng.permutation(nb)[:4096].tolist()
+    cow = dict(zip(blocks[:2048], blocks[2048:]))
+    cow_pairs = torch.tensor(list(cow.items()), dtype=torch.int64, device=dev)
+    ms_cow, _ = time_loop(lambda: copy_blocks(kv, cow_pairs), steps, warmup)  # kernel: pairs on the device
+    ms_cow_dict, _ = time_loop(lambda: copy_blocks(kv, cow), max(3, steps // 4), 2)  # with the host upload
+    cow_bytes = 2 * len(cow) * 2 * page
+    host = torch.empty((1, 2, 512) + tuple(kv.shape[3:]), dtype=kv.dtype).pin_memory()
+    out_map = dict(zip(blocks[:512], range(512)))
+    in_map = dict(zip(range(512), blocks[512:1024]))
+    ms_out, _ = time_loop(lambda: swap_blocks(kv, host, out_map), max(3, steps // 4), 2)
+    ms_in, _ = time_loop(lambda: swap_blocks(host, kv, in_map), max(3, steps // 4), 2)
+    swap_bytes = 512 * 2 * page
+    del b, kv, host
+    torch.cuda.empty_cache()
+    return {"workload": "2048 copy-on-write page pairs in the C2 pool (K and V, 32 KB pages); swap of 512 "
+                        "pages to / from a pinned host cache",
+            "cow_us": round(ms_cow * 1e3, 2), "cow_GBps": round(cow_bytes / (ms_cow * 1e-3) / 1e9, 1),
+            "cow_dict_us": round(ms_cow_dict * 1e3, 2),
+            "cow_frac_hbm": round(cow_bytes / (ms_cow * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "swap_out_us": round(ms_out * 1e3, 2), "swap_out_GBps": round(swap_bytes / (ms_out * 1e-3) / 1e9, 1),
+            "swap_in_us": round(ms_in * 1e3, 2), "swap_in_GBps": round(swap_bytes / (ms_in * 1e-3) / 1e9, 1)}
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -289,6 +327,9 @@ def main() -> int:
         return 0
     if args.only == "w4a16":  # profiling aid: the C5 section alone
         print(json.dumps({"w4a16": w4a16_section(dev, args.steps, args.warmup)}), flush=True)
+        return 0
+    if args.only == "block_copy":  # profiling aid: the page-copy section alone
+        print(json.dumps({"block_copy": block_copy_section(dev, args.steps, args.warmup)}), flush=True)
         return 0
 
     # ---- C2: headline decode step ------------------------------------------------
@@ -405,6 +446,9 @@ def main() -> int:
 
         # ---- C5: W4A16 linears ------------------------------------------------------
         result["w4a16"] = w4a16_section(dev, args.steps, args.warmup)
+
+        # ---- page copies (copy-on-write, swap) -------------------------------------
+        result["block_copy"] = block_copy_section(dev, args.steps, args.warmup)
 
     if not args.no_cpu_baseline:
         b = workloads.llama_decode(device=dev, seed=args.seed)

@@ -154,6 +154,29 @@ int ss_w4a16_gemm(const void* x, void* out, const int32_t* qweight, const void* 
                   int64_t x_stride, int64_t o_stride, int act_dtype, int scale_dtype,
                   void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * KV page copies: for each pair i, page pairs[2i + 1] of dst <- page pairs[2i] of
+ * src, in every plane p in [0, planes) (a plane is one (layer, K/V) of
+ * kv_cache[L, 2, NB, ...], so planes = 2L for a contiguous cache). Page b of plane
+ * p starts at base + p * plane_stride + b * block_stride (bytes) and is page_bytes
+ * contiguous bytes (block_size * n_kv * head_dim * element size). pairs is a
+ * device int64 array [n_pairs, 2]; pairs with an id outside [0, *_blocks) are
+ * skipped. A byte copy, bit exact.
+ *   dst == src: replaces copy_blocks_ref (slipstream/kernels/attention_ref.py:92-94),
+ *     the copy-on-write copy of slipstream/memory/block_manager.py:297-298. All
+ *     pairs of one call run at once: a destination that is also a source, or a
+ *     repeated destination, makes the order matter -- split such lists into
+ *     ordered calls (the Python wrapper does).
+ *   one side a pinned host cache (hipHostMalloc, torch pin_memory): the swap
+ *     copies of block_manager.py:196-200 (out) and :220-225 (in), read or written
+ *     through the host memory's device mapping. Pageable host memory is
+ *     SS_ERR_INVALID.
+ */
+int ss_copy_blocks(void* dst, const void* src, int64_t planes, int64_t dst_plane_stride,
+                   int64_t dst_block_stride, int64_t dst_blocks, int64_t src_plane_stride,
+                   int64_t src_block_stride, int64_t src_blocks, int64_t page_bytes,
+                   const int64_t* pairs, int64_t n_pairs, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -60,6 +60,21 @@ def reshape_and_cache(
         kv_cache[layer_idx, 1, s // block_size, s % block_size] = v[n]
 
 
+def copy_blocks(kv_cache: np.ndarray, pairs) -> None:
+    """In place: ``kv_cache[:, :, dst] = kv_cache[:, :, src]`` for each (src, dst), one
+    pair after the other (attention_ref.py:92-94 iterates its dict in order). The swap
+    copies of block_manager.py:196-200,220-225 are the same page copy between two arrays
+    (``swap_blocks``). Any dtype; usually the raw 16-bit patterns (bit exact)."""
+    for s, d in pairs:
+        kv_cache[:, :, d] = kv_cache[:, :, s]
+
+
+def swap_blocks(src_cache: np.ndarray, dst_cache: np.ndarray, pairs) -> None:
+    """In place: ``dst_cache[:, :, dst] = src_cache[:, :, src]`` for each (src, dst)."""
+    for s, d in pairs:
+        dst_cache[:, :, d] = src_cache[:, :, s]
+
+
 def gather_kv(
     kv_cache: np.ndarray, layer_idx: int, block_table: np.ndarray, seq_len: int, block_size: int
 ) -> tuple[np.ndarray, np.ndarray, np.ndarray]:

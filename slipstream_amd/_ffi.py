@@ -59,6 +59,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i32,
         [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i64, _i64, _i32, _i32, _vp, _i64, _vp],
     ),
+    "ss_copy_blocks": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -1,5 +1,6 @@
 """HIP (gfx950) kernels behind the reference's ``slipstream.kernels`` call signatures."""
 
+from slipstream_amd.kernels.block_copy import copy_blocks, swap_blocks
 from slipstream_amd.kernels.paged_attention import (
     paged_attention,
     paged_attention_decode,
@@ -10,10 +11,12 @@ from slipstream_amd.kernels.quant_gemm import w4a16_gemm
 from slipstream_amd.kernels.reshape_and_cache import reshape_and_cache
 
 __all__ = [
+    "copy_blocks",
     "paged_attention",
     "paged_attention_decode",
     "paged_attention_prefill",
     "paged_attention_varlen",
     "reshape_and_cache",
+    "swap_blocks",
     "w4a16_gemm",
 ]

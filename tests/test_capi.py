@@ -23,7 +23,7 @@ def test_header_declares_entry_points():
     names = declared_functions()
     for required in ("ss_reshape_and_cache", "ss_paged_attention", "ss_paged_attention_varlen",
                      "ss_paged_attention_workspace_size", "ss_status_string", "ss_last_error",
-                     "ss_w4a16_gemm", "ss_w4a16_workspace_size"):
+                     "ss_w4a16_gemm", "ss_w4a16_workspace_size", "ss_copy_blocks"):
         assert required in names
 
 
@@ -90,3 +90,14 @@ def test_w4a16_argument_errors_need_no_device():
     st = lib.ss_w4a16_gemm(None, None, None, None, None, 1, 8, 256, 128, 256, 8, _ffi.SS_DTYPE_BF16,
                            7, None, 0, None)
     assert st == _ffi.SS_ERR_UNSUPPORTED
+
+
+def test_copy_blocks_argument_errors_need_no_device():
+    """Empty copies touch nothing; negative extents and null pointers are SS_ERR_INVALID."""
+    from slipstream_amd import _ffi
+
+    lib = _ffi.lib()
+    assert lib.ss_copy_blocks(None, None, 2, 0, 0, 0, 0, 0, 0, 32768, None, 0, None) == _ffi.SS_OK
+    assert lib.ss_copy_blocks(None, None, -1, 0, 0, 0, 0, 0, 0, 32768, None, 1, None) == _ffi.SS_ERR_INVALID
+    assert lib.ss_copy_blocks(None, None, 2, 0, 0, 4, 0, 0, 4, 32768, None, 1, None) == _ffi.SS_ERR_INVALID
+    assert b"null pointer" in lib.ss_last_error()

@@ -284,3 +284,55 @@ def test_known_answers_attention():
         out = ora.paged_attention(np.array(case["q"], dtype=np.float64), kv, np.array(case["block_tables"]),
                                   np.array(case["seq_lens"]), 0, case["scale"], case["block_size"])
         np.testing.assert_allclose(out, np.array(case["expected"]), atol=1e-12, err_msg=case["name"])
+
+
+# ---------------------------------------------------------------- page copies
+
+
+def _pages(n_layers=2, nb=9, bs=4, n_kv=2, d=8, seed=0):
+    return np.random.default_rng(seed).integers(0, 1 << 16, (n_layers, 2, nb, bs, n_kv, d)).astype(np.uint16)
+
+
+def test_copy_blocks_closed_form_and_order():
+    """attention_ref.py:92-94: page dst of every (layer, K/V) becomes page src; every other
+    page is untouched; pairs apply in order, so a chain (0->1, 1->2) moves page 0 to 2."""
+    kv = _pages()
+    before = kv.copy()
+    ora.copy_blocks(kv, [(3, 5), (0, 1), (1, 2), (7, 7)])
+    assert np.array_equal(kv[:, :, 5], before[:, :, 3])
+    assert np.array_equal(kv[:, :, 1], before[:, :, 0])
+    assert np.array_equal(kv[:, :, 2], before[:, :, 0])  # sequential: 1 already holds page 0
+    untouched = [b for b in range(kv.shape[2]) if b not in (1, 2, 5)]
+    assert np.array_equal(kv[:, :, untouched], before[:, :, untouched])
+    # repeated destination: the last pair wins
+    kv2 = before.copy()
+    ora.copy_blocks(kv2, [(3, 4), (6, 4)])
+    assert np.array_equal(kv2[:, :, 4], before[:, :, 6])
+
+
+def test_swap_round_trip_is_identity_on_the_pages():
+    gpu = _pages(seed=1)
+    cpu = np.zeros((2, 2, 5, 4, 2, 8), np.uint16)
+    ora.swap_blocks(gpu, cpu, [(8, 0), (2, 3)])
+    back = np.zeros_like(gpu)
+    ora.swap_blocks(cpu, back, [(0, 1), (3, 6)])
+    assert np.array_equal(back[:, :, 1], gpu[:, :, 8]) and np.array_equal(back[:, :, 6], gpu[:, :, 2])
+
+
+def test_ordered_batches_reproduce_sequential_copies():
+    """The wrapper's batching: running each batch all at once (reads before writes) gives
+    the one-by-one result, on random pair lists full of chains and repeats."""
+    from slipstream_amd.kernels.block_copy import ordered_batches
+
+    rng = np.random.default_rng(5)
+    for _ in range(200):
+        pairs = [tuple(int(v) for v in rng.integers(0, 6, 2)) for _ in range(rng.integers(1, 9))]
+        seq = _pages(n_layers=1, nb=6, bs=1, n_kv=1, d=2, seed=int(rng.integers(1 << 30)))
+        par = seq.copy()
+        ora.copy_blocks(seq, pairs)
+        for batch in ordered_batches(pairs):
+            snap = par.copy()
+            for s, d in batch:
+                par[:, :, d] = snap[:, :, s]
+        assert np.array_equal(seq, par), pairs
+        assert sum(len(b) for b in ordered_batches(pairs)) == len(pairs)
