@@ -42,8 +42,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the host-side reference timing")
     ap.add_argument("--skip-extra", action="store_true", help="headline only (no packed / prefix lines)")
-    ap.add_argument("--only", choices=["all", "w4a16", "block_copy", "copy"], default="all",
-                    help="w4a16 / block_copy: run that section alone; copy: 1 GiB device copies of known "
+    ap.add_argument("--only", choices=["all", "w4a16", "block_copy", "rope_cache", "copy"], default="all",
+                    help="w4a16 / block_copy / rope_cache: run that section alone; copy: 1 GiB device copies of known "
                          "size, the calibration kernel for the FETCH_SIZE/WRITE_SIZE counters (profiling aids)")
     return ap.parse_args()
 
@@ -289,6 +289,47 @@ def block_copy_section(dev, steps: int, warmup: int) -> dict:
             "swap_in_us": round(ms_in * 1e3, 2), "swap_in_GBps": round(swap_bytes / (ms_in * 1e-3) / 1e9, 1)}
 
 
+def rope_cache_section(dev, steps: int, warmup: int) -> dict:
+    """Rotary embedding + KV scatter, fused, against the unfused pair the attention layer
+    runs (torch's apply_rotary_pos_emb arithmetic on Q and K, then the scatter), at the C2
+    decode step (256 tokens) and the C3 packed step (2240 tokens), Llama-3-8B shape.
+    Bytes of the fused op: Q, K, V, cos, sin read once; rotated Q, K and V written once."""
+    import torch
+
+    from slipstream_amd.kernels import reshape_and_cache, rope_and_cache
+
+    out = {"workload": "fused RoPE + KV scatter vs unfused (torch RoPE on Q, K then the scatter), "
+                       "Llama-3-8B shape, bf16, packed token stream"}
+    g = torch.Generator(device=dev).manual_seed(0)
+    n_q, n_kv, d = 32, 8, 128
+    for name, n in (("c2_256_tokens", 256), ("c3_2240_tokens", 2240)):
+        q = torch.randn(n, n_q, d, generator=g, device=dev).to(torch.bfloat16)
+        k = torch.randn(n, n_kv, d, generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn(n, n_kv, d, generator=g, device=dev).to(torch.bfloat16)
+        pos = torch.arange(n, device=dev, dtype=torch.float32)[:, None] * 0.01
+        cos, sin = torch.cos(pos.expand(n, d)).to(torch.bfloat16), torch.sin(pos.expand(n, d)).to(torch.bfloat16)
+        kv = torch.zeros(1, 2, (n + 15) // 16 + 8, 16, n_kv, d, dtype=torch.bfloat16, device=dev)
+        slots = torch.randperm(kv.shape[2] * 16, generator=g, device=dev)[:n]
+
+        def fused():
+            return rope_and_cache(q, k, v, cos, sin, kv, slots, 0, 16)
+
+        def unfused():
+            c, s_ = cos[:, None], sin[:, None]
+            rot = lambda x: torch.cat((-x[..., d // 2:], x[..., : d // 2]), dim=-1)  # noqa: E731
+            qe = q * c + rot(q) * s_
+            ke = k * c + rot(k) * s_
+            reshape_and_cache(ke, v, kv, slots, 0, 16)
+            return qe
+
+        ms_f = graph_time(fused, 8, max(3, steps // 8))
+        ms_u = graph_time(unfused, 8, max(3, steps // 8))
+        nbytes = n * ((n_q + 2 * n_kv) * d * 2 * 2 + 2 * d * 2)
+        out[name] = {"fused_us": round(ms_f * 1e3, 2), "unfused_us": round(ms_u * 1e3, 2),
+                     "fused_GBps": round(nbytes / (ms_f * 1e-3) / 1e9, 1), "bytes": nbytes}
+    return out
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -330,6 +371,9 @@ def main() -> int:
         return 0
     if args.only == "block_copy":  # profiling aid: the page-copy section alone
         print(json.dumps({"block_copy": block_copy_section(dev, args.steps, args.warmup)}), flush=True)
+        return 0
+    if args.only == "rope_cache":  # profiling aid: the fused RoPE + scatter section alone
+        print(json.dumps({"rope_cache": rope_cache_section(dev, args.steps, args.warmup)}), flush=True)
         return 0
 
     # ---- C2: headline decode step ------------------------------------------------
@@ -449,6 +493,9 @@ def main() -> int:
 
         # ---- page copies (copy-on-write, swap) -------------------------------------
         result["block_copy"] = block_copy_section(dev, args.steps, args.warmup)
+
+        # ---- fused RoPE + scatter ---------------------------------------------------
+        result["rope_cache"] = rope_cache_section(dev, args.steps, args.warmup)
 
     if not args.no_cpu_baseline:
         b = workloads.llama_decode(device=dev, seed=args.seed)

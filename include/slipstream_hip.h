@@ -177,6 +177,33 @@ int ss_copy_blocks(void* dst, const void* src, int64_t planes, int64_t dst_plane
                    int64_t src_block_stride, int64_t src_blocks, int64_t page_bytes,
                    const int64_t* pairs, int64_t n_pairs, void* stream);
 
+/*
+ * Rotary embedding of Q and K fused with the KV scatter: replaces
+ * apply_rotary_pos_emb (slipstream/models/layers/rope.py:20-36) followed by
+ * reshape_and_cache (slipstream/kernels/reshape_and_cache.py:10-27) as
+ * Attention.forward runs them (slipstream/models/layers/attention.py:163,171-174);
+ * the reference's fuse seam is slipstream/kernels/fused_rope.py:168-181.
+ *   q_out[n, h]          = rope(q[n, h])            (h < n_q)
+ *   k_cache[slot(n), h]  = rope(k[n, h])            (h < n_kv, slot(n) >= 0)
+ *   v_cache[slot(n), h]  = v[n, h]
+ * rope(x) = x * cos[n] + rotate_half(x) * sin[n], rotate_half(x) = cat(-x2, x1),
+ * rounded as the reference's torch ops round: each product and the sum computed
+ * in fp32 and rounded to dtype (no fused multiply-add for fp32) -- bit identical.
+ * Token n = o * n_inner + i (o < n_outer, i < n_inner). Strides are in elements:
+ * q/k/v/o strides are (outer, inner, head) with unit head_dim stride; cos/sin
+ * strides are (outer, inner) with unit head_dim stride (0 broadcasts); c_strides
+ * are the cache planes' (block, position, head) strides as for
+ * ss_reshape_and_cache. Slots < 0 or >= num_slots are skipped. head_dim even;
+ * dtype SS_DTYPE_BF16/F16/F32 for every tensor (cos/sin in the tensors' dtype,
+ * as RotaryEmbedding returns them, rope.py:106).
+ */
+int ss_rope_and_cache(const void* q, const void* k, const void* v, const void* cos, const void* sin,
+                      void* q_out, void* k_cache, void* v_cache, const int64_t* slot_mapping,
+                      int64_t n_outer, int64_t n_inner, int n_q, int n_kv, int head_dim, int block_size,
+                      int64_t num_slots, const int64_t q_strides[3], const int64_t k_strides[3],
+                      const int64_t v_strides[3], const int64_t o_strides[3], const int64_t cos_strides[2],
+                      const int64_t sin_strides[2], const int64_t c_strides[3], int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,6 +9,7 @@ from slipstream_amd.kernels.paged_attention import (
 )
 from slipstream_amd.kernels.quant_gemm import w4a16_gemm
 from slipstream_amd.kernels.reshape_and_cache import reshape_and_cache
+from slipstream_amd.kernels.rope_cache import rope_and_cache
 
 __all__ = [
     "copy_blocks",
@@ -17,6 +18,7 @@ __all__ = [
     "paged_attention_prefill",
     "paged_attention_varlen",
     "reshape_and_cache",
+    "rope_and_cache",
     "swap_blocks",
     "w4a16_gemm",
 ]

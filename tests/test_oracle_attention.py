@@ -336,3 +336,48 @@ def test_ordered_batches_reproduce_sequential_copies():
                 par[:, :, d] = snap[:, :, s]
         assert np.array_equal(seq, par), pairs
         assert sum(len(b) for b in ordered_batches(pairs)) == len(pairs)
+
+
+# ---------------------------------------------------------------- rotary embedding
+
+
+def test_rotate_half_known_answer():
+    """test_layers_reference.py:36-42: [a, b, c, d] -> [-c, -d, a, b]."""
+    from oracle import rope
+
+    x = np.array([[1.0, 2.0, 3.0, 4.0], [5.0, 6.0, 7.0, 8.0]])
+    assert np.array_equal(rope.rotate_half(x)[0], [-3.0, -4.0, 1.0, 2.0])
+
+
+@pytest.mark.parametrize("dtype,tdt", [("bf16", torch.bfloat16), ("f16", torch.float16), ("f32", torch.float32)])
+def test_apply_rope_matches_torch_elementwise_rounding(dtype, tdt):
+    """The reference formula evaluated by torch's CPU elementwise ops (the arithmetic the
+    reference runs, rope.py:33-35), on random q and random cos/sin as the reference's
+    own fused-kernel test uses (test_fused_kernels.py:37-46): bit identical."""
+    from oracle import rope
+
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(2, 4, 8, 64, generator=g).to(tdt)
+    cos = torch.randn(2, 8, 64, generator=g).to(tdt)
+    sin = torch.randn(2, 8, 64, generator=g).to(tdt)
+    c, s = cos.unsqueeze(1), sin.unsqueeze(1)
+    half = q.shape[-1] // 2
+    want = q * c + torch.cat((-q[..., half:], q[..., :half]), dim=-1) * s
+    got = rope.apply_rope(q.double().numpy(), c.double().numpy(), s.double().numpy(), dtype)
+    assert np.array_equal(got, want.double().numpy())
+
+
+def test_rope_is_a_rotation_in_exact_arithmetic():
+    """With tables from angles (both halves equal) and no rounding: each (i, i + D/2)
+    pair keeps its norm, and rotating by a then by b equals rotating by a + b."""
+    from oracle import rope
+
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((5, 16))
+    a, b = rng.uniform(-3, 3, (5, 8)), rng.uniform(-3, 3, (5, 8))
+    def rot(v, ang):
+        c, s = np.cos(np.concatenate((ang, ang), -1)), np.sin(np.concatenate((ang, ang), -1))
+        return v * c + rope.rotate_half(v) * s
+    y = rot(x, a)
+    assert np.allclose(y[:, :8] ** 2 + y[:, 8:] ** 2, x[:, :8] ** 2 + x[:, 8:] ** 2)
+    assert np.allclose(rot(rot(x, a), b), rot(x, a + b))
