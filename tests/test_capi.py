@@ -23,7 +23,7 @@ def test_header_declares_entry_points():
     names = declared_functions()
     for required in ("ss_reshape_and_cache", "ss_paged_attention", "ss_paged_attention_varlen",
                      "ss_paged_attention_workspace_size", "ss_status_string", "ss_last_error",
-                     "ss_w4a16_gemm", "ss_w4a16_workspace_size", "ss_copy_blocks"):
+                     "ss_w4a16_gemm", "ss_w4a16_workspace_size", "ss_copy_blocks", "ss_rope_and_cache"):
         assert required in names
 
 
@@ -101,3 +101,19 @@ def test_copy_blocks_argument_errors_need_no_device():
     assert lib.ss_copy_blocks(None, None, -1, 0, 0, 0, 0, 0, 0, 32768, None, 1, None) == _ffi.SS_ERR_INVALID
     assert lib.ss_copy_blocks(None, None, 2, 0, 0, 4, 0, 0, 4, 32768, None, 1, None) == _ffi.SS_ERR_INVALID
     assert b"null pointer" in lib.ss_last_error()
+
+
+def test_rope_and_cache_argument_errors_need_no_device():
+    """Odd head_dim and unknown dtypes are rejected on the host; no tokens is a no-op."""
+    from slipstream_amd import _ffi
+
+    lib = _ffi.lib()
+    st3 = _ffi.i64_array([0, 0, 0])
+    st2 = _ffi.i64_array([0, 0])
+    args = lambda n, d, dt: (None, None, None, None, None, None, None, None, None, 1, n, 4, 2, d, 16, 64,  # noqa: E731
+                             st3, st3, st3, st3, st2, st2, st3, dt, None)
+    assert lib.ss_rope_and_cache(*args(0, 128, _ffi.SS_DTYPE_BF16)) == _ffi.SS_OK
+    assert lib.ss_rope_and_cache(*args(4, 7, _ffi.SS_DTYPE_BF16)) == _ffi.SS_ERR_INVALID
+    assert b"even" in lib.ss_last_error()
+    assert lib.ss_rope_and_cache(*args(4, 128, 9)) == _ffi.SS_ERR_UNSUPPORTED
+    assert lib.ss_rope_and_cache(*args(4, 128, _ffi.SS_DTYPE_BF16)) == _ffi.SS_ERR_INVALID  # null pointers
