@@ -450,6 +450,24 @@ def main() -> int:
                                           m.scale, 16, m.max_query_len)
 
         ms_mixed, _ = time_loop(mixed, max(10, args.steps // 2), args.warmup)
+
+        # the same step as one layer runs it with nothing built on the host: metadata on
+        # the device, RoPE fused with the scatter, then the varlen attention
+        from slipstream_amd.kernels import packed_attention
+        from slipstream_amd.paged_cache import build_packed_step
+
+        ql_dev = torch.tensor(m.query_lens, dtype=torch.int32, device=dev)
+        prior_dev = m.context_lens.to(torch.int32) - ql_dev
+        pos = torch.arange(m.total_tokens, device=dev, dtype=torch.float32)[:, None] * 0.01
+        cos_t = torch.cos(pos.expand(-1, m.head_dim)).to(torch.bfloat16)
+        sin_t = torch.sin(pos.expand(-1, m.head_dim)).to(torch.bfloat16)
+
+        def layer_step():
+            meta = build_packed_step(m.block_tables, prior_dev, ql_dev, 16, m.total_tokens, m.max_query_len)
+            return packed_attention(m.q, m.k_new, m.v_new, cos_t, sin_t, m.kv_cache, meta, 0, m.scale, 16)
+
+        ms_layer, _ = time_loop(layer_step, max(10, args.steps // 2), args.warmup)
+        ms_layer_graph = graph_time(layer_step, 4, max(3, args.steps // 8))
         dec_kv = sum(c for c, ql in zip(m.ctx_host, m.query_lens) if ql == 1) * 2 * m.n_kv * m.head_dim * 2
         pre_kv = sum(c for c, ql in zip(m.ctx_host, m.query_lens) if ql > 1) * 2 * m.n_kv * m.head_dim * 2
         flops = prefill_flops(m)
@@ -463,6 +481,9 @@ def main() -> int:
             "roofline_frac": round(roof_us / (ms_mixed * 1e3), 4),
             "decode_kv_bytes": dec_kv,
             "prefill_flops": flops,
+            "layer_step_us": round(ms_layer * 1e3, 2),
+            "layer_step_graph_us": round(ms_layer_graph * 1e3, 2),
+            "layer_step": "device-built metadata + fused RoPE/scatter + varlen attention (no host lists)",
         }
         del m
         torch.cuda.empty_cache()

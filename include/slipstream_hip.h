@@ -204,6 +204,26 @@ int ss_rope_and_cache(const void* q, const void* k, const void* v, const void* c
                       const int64_t v_strides[3], const int64_t o_strides[3], const int64_t cos_strides[2],
                       const int64_t sin_strides[2], const int64_t c_strides[3], int dtype, void* stream);
 
+/*
+ * Packed-step metadata on the device: replaces the host-list building of
+ * build_paged_forward (slipstream/memory/paged_cache.py:71-109) and the packed
+ * description ss_paged_attention_varlen takes. From block_tables [batch, >= max_blocks]
+ * (int32, row stride bt_stride, -1 padded), prior_lens [batch] (KV tokens before the
+ * step) and query_lens [batch] (new tokens), all int32 on the device:
+ *   cu_seqlens [batch + 1]  exclusive prefix sum of query_lens;
+ *   context_lens [batch]    prior_lens + query_lens (the reference's seq_lens);
+ *   slot_mapping [total_tokens] int64: token j of sequence b (position
+ *     p = prior_lens[b] + j) -> table[b][p / block_size] * block_size + p % block_size,
+ *     the slot BlockManagerImpl.append_slot hands out when earlier blocks are full
+ *     (block_manager.py:141-159); -1 past the table or on a negative entry.
+ * Negative lengths count as 0; tokens past total_tokens are not written. Nothing
+ * is read back to the host, so a step built this way can be graph-captured.
+ */
+int ss_build_step_metadata(const int32_t* block_tables, int64_t bt_stride, int max_blocks,
+                           const int32_t* prior_lens, const int32_t* query_lens, int batch,
+                           int block_size, int32_t* cu_seqlens, int32_t* context_lens,
+                           int64_t* slot_mapping, int64_t total_tokens, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

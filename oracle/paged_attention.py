@@ -60,6 +60,28 @@ def reshape_and_cache(
         kv_cache[layer_idx, 1, s // block_size, s % block_size] = v[n]
 
 
+def build_step_metadata(tables: list[list[int]], prior_lens, query_lens, block_size: int):
+    """Packed metadata of one step (paged_cache.py:71-109 with the packed description):
+    ``cu_seqlens`` = [0] + cumsum(query_lens), ``context_lens`` = prior + query, and the
+    slot of token j of sequence b at position p = prior[b] + j:
+    ``tables[b][p // bs] * bs + p % bs`` (-1 past the table or on a negative entry).
+    Negative lengths count as 0."""
+    q = [max(int(v), 0) for v in query_lens]
+    p0 = [max(int(v), 0) for v in prior_lens]
+    cu = [0]
+    for v in q:
+        cu.append(cu[-1] + v)
+    slots = []
+    for b, table in enumerate(tables):
+        for j in range(q[b]):
+            pos = p0[b] + j
+            bi = pos // block_size
+            e = table[bi] if bi < len(table) else -1
+            slots.append(e * block_size + pos % block_size if e >= 0 else -1)
+    ctx = [a + b for a, b in zip(p0, q)]
+    return np.array(cu, np.int32), np.array(ctx, np.int32), np.array(slots, np.int64)
+
+
 def copy_blocks(kv_cache: np.ndarray, pairs) -> None:
     """In place: ``kv_cache[:, :, dst] = kv_cache[:, :, src]`` for each (src, dst), one
     pair after the other (attention_ref.py:92-94 iterates its dict in order). The swap

@@ -98,3 +98,50 @@ def pack_step(fwd: PagedForward, query_lens: list[int]) -> PackedStep:
         max_query_len=max(query_lens) if query_lens else 0,
         total_tokens=cu[-1],
     )
+
+
+def build_packed_step(
+    block_tables: torch.Tensor,
+    prior_lens: torch.Tensor,
+    query_lens: torch.Tensor,
+    block_size: int,
+    total_tokens: int,
+    max_query_len: int,
+) -> PackedStep:
+    """Packed metadata of one step built on the device (``ss_build_step_metadata``).
+
+    Replaces the host-list building of ``build_paged_forward`` (``paged_cache.py:71-109``):
+    ``block_tables [B, max_blocks]``, ``prior_lens [B]`` (KV tokens before the step) and
+    ``query_lens [B]`` stay on the device; the new tokens' slots are those
+    ``append_slot`` hands out (``block_manager.py:141-159``). ``total_tokens`` and
+    ``max_query_len`` are the host's own copies (the scheduler chose the lengths); no
+    value is read back from the device.
+    """
+    from slipstream_amd import _ffi
+
+    if block_tables.ndim != 2 or block_tables.dtype != torch.int32:
+        raise ValueError(f"block_tables must be [B, max_blocks] int32, got {tuple(block_tables.shape)} "
+                         f"{block_tables.dtype}")
+    batch = block_tables.shape[0]
+    for t, name in ((prior_lens, "prior_lens"), (query_lens, "query_lens")):
+        if t.shape != (batch,) or t.dtype != torch.int32 or t.device != block_tables.device:
+            raise ValueError(f"{name} must be [{batch}] int32 on {block_tables.device}, got {tuple(t.shape)} "
+                             f"{t.dtype} on {t.device}")
+    if block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()
+    device = block_tables.device
+    # every entry is written by the kernel (no fill: the step may be graph-captured)
+    cu = torch.empty(batch + 1, dtype=torch.int32, device=device) if batch else torch.zeros(1, dtype=torch.int32)
+    ctx = torch.empty(batch, dtype=torch.int32, device=device)
+    slots = torch.empty(max(total_tokens, 0), dtype=torch.int64, device=device)
+    if batch:
+        if device.type != "cuda":
+            raise _ffi.KernelError(f"build_packed_step: slipstream_amd runs on HIP devices only; got {device}")
+        lib = _ffi.lib()
+        status = lib.ss_build_step_metadata(
+            block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1], prior_lens.contiguous().data_ptr(),
+            query_lens.contiguous().data_ptr(), batch, block_size, cu.data_ptr(), ctx.data_ptr(),
+            slots.data_ptr(), slots.numel(), _ffi.stream_ptr(device))
+        _ffi.check(status, "build_step_metadata")
+    return PackedStep(cu_seqlens=cu, context_lens=ctx, block_tables=block_tables, slot_mapping=slots,
+                      max_query_len=max_query_len, total_tokens=total_tokens)

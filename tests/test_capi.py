@@ -23,7 +23,8 @@ def test_header_declares_entry_points():
     names = declared_functions()
     for required in ("ss_reshape_and_cache", "ss_paged_attention", "ss_paged_attention_varlen",
                      "ss_paged_attention_workspace_size", "ss_status_string", "ss_last_error",
-                     "ss_w4a16_gemm", "ss_w4a16_workspace_size", "ss_copy_blocks", "ss_rope_and_cache"):
+                     "ss_w4a16_gemm", "ss_w4a16_workspace_size", "ss_copy_blocks", "ss_rope_and_cache",
+                     "ss_build_step_metadata"):
         assert required in names
 
 
@@ -117,3 +118,13 @@ def test_rope_and_cache_argument_errors_need_no_device():
     assert b"even" in lib.ss_last_error()
     assert lib.ss_rope_and_cache(*args(4, 128, 9)) == _ffi.SS_ERR_UNSUPPORTED
     assert lib.ss_rope_and_cache(*args(4, 128, _ffi.SS_DTYPE_BF16)) == _ffi.SS_ERR_INVALID  # null pointers
+
+
+def test_build_step_metadata_argument_errors_need_no_device():
+    from slipstream_amd import _ffi
+
+    lib = _ffi.lib()
+    assert lib.ss_build_step_metadata(None, 0, 0, None, None, 0, 16, None, None, None, 0, None) == _ffi.SS_OK
+    assert lib.ss_build_step_metadata(None, 0, 0, None, None, 2, 0, None, None, None, 0, None) == _ffi.SS_ERR_INVALID
+    assert lib.ss_build_step_metadata(None, 0, 0, None, None, 2, 16, None, None, None, 0, None) == _ffi.SS_ERR_INVALID
+    assert b"null pointer" in lib.ss_last_error()

@@ -381,3 +381,61 @@ def test_rope_is_a_rotation_in_exact_arithmetic():
     y = rot(x, a)
     assert np.allclose(y[:, :8] ** 2 + y[:, 8:] ** 2, x[:, :8] ** 2 + x[:, 8:] ** 2)
     assert np.allclose(rot(rot(x, a), b), rot(x, a + b))
+
+
+# ---------------------------------------------------------------- step metadata
+
+
+class _MiniBlockManager:
+    """block_manager.py:141-159,282-287 restated for the test: a token goes to the first
+    not-full block of the table (a fresh block from the free list when none is)."""
+
+    def __init__(self, n_blocks: int, block_size: int, seed: int):
+        self.bs = block_size
+        self.free = np.random.default_rng(seed).permutation(n_blocks).tolist()
+        self.fill = [0] * n_blocks
+
+    def append_slot(self, table: list[int]) -> tuple[int, int]:
+        idx = next((i for i, b in enumerate(table) if self.fill[b] < self.bs), None)
+        if idx is None:
+            table.append(self.free.pop())
+            idx = len(table) - 1
+        bid = table[idx]
+        off = self.fill[bid]
+        self.fill[bid] += 1
+        return bid, off
+
+
+def test_step_metadata_matches_append_slot():
+    """The slot rule of the device builder (table[p // bs] * bs + p % bs) equals the slots
+    append_slot hands out, on random prefill + step sequences; cu_seqlens and
+    context_lens are the packed description."""
+    rng = np.random.default_rng(7)
+    for trial in range(20):
+        bs = int(rng.choice([1, 4, 16]))
+        bm = _MiniBlockManager(4096, bs, seed=trial)
+        batch = int(rng.integers(1, 12))
+        tables = [[] for _ in range(batch)]
+        prior = rng.integers(0, 70, batch).tolist()
+        q = rng.integers(0, 20, batch).tolist()
+        for b in range(batch):
+            for _ in range(prior[b]):
+                bm.append_slot(tables[b])
+        want = []
+        for b in range(batch):
+            for _ in range(q[b]):
+                bid, off = bm.append_slot(tables[b])
+                want.append(bid * bs + off)
+        cu, ctx, slots = ora.build_step_metadata(tables, prior, q, bs)
+        assert slots.tolist() == want
+        assert cu.tolist() == [0] + np.cumsum(q).tolist()
+        assert ctx.tolist() == [a + b for a, b in zip(prior, q)]
+
+
+def test_step_metadata_edges():
+    """Positions past the table and negative entries give -1; negative lengths count as 0."""
+    cu, ctx, slots = ora.build_step_metadata([[3, -1], [5]], [6, 0], [4, -2], 8)
+    assert cu.tolist() == [0, 4, 4] and ctx.tolist() == [10, 0]
+    assert slots.tolist() == [3 * 8 + 6, 3 * 8 + 7, -1, -1]  # positions 8, 9 sit on the hole
+    _, _, past = ora.build_step_metadata([[2]], [3], [3], 4)
+    assert past.tolist() == [2 * 4 + 3, -1, -1]  # positions 4, 5 are past the one-block table
