@@ -42,8 +42,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the host-side reference timing")
     ap.add_argument("--skip-extra", action="store_true", help="headline only (no packed / prefix lines)")
-    ap.add_argument("--only", choices=["all", "w4a16", "block_copy", "rope_cache", "copy"], default="all",
-                    help="w4a16 / block_copy / rope_cache: run that section alone; copy: 1 GiB device copies of known "
+    ap.add_argument("--only", choices=["all", "w4a16", "block_copy", "rope_cache", "norm_act", "copy"], default="all",
+                    help="w4a16 / block_copy / rope_cache / norm_act: run that section alone; copy: 1 GiB device copies of known "
                          "size, the calibration kernel for the FETCH_SIZE/WRITE_SIZE counters (profiling aids)")
     return ap.parse_args()
 
@@ -330,6 +330,40 @@ def rope_cache_section(dev, steps: int, warmup: int) -> dict:
     return out
 
 
+def norm_act_section(dev, steps: int, warmup: int) -> dict:
+    """RMSNorm (with residual) and SwiGLU kernels against the reference's eager torch
+    arithmetic at a 256-token decode step of Llama-3-8B (hidden 4096, intermediate 14336),
+    bf16. Bytes: inputs read once, output written once."""
+    import torch
+    import torch.nn.functional as F
+
+    from slipstream_amd.kernels import fused_rmsnorm, fused_swiglu
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(256, 4096, generator=g, device=dev).to(torch.bfloat16)
+    r = torch.randn(256, 4096, generator=g, device=dev).to(torch.bfloat16)
+    w = torch.ones(4096, device=dev, dtype=torch.bfloat16)
+    gate = torch.randn(256, 14336, generator=g, device=dev).to(torch.bfloat16)
+    up = torch.randn(256, 14336, generator=g, device=dev).to(torch.bfloat16)
+
+    def eager_norm():
+        s = x + r
+        s32 = s.float()
+        return w * (s32 * torch.rsqrt(s32.pow(2).mean(-1, keepdim=True) + 1e-6)).to(s.dtype)
+
+    ms_n = graph_time(lambda: fused_rmsnorm(x, w, r, 1e-6), 16, max(3, steps // 8))
+    ms_ne = graph_time(eager_norm, 16, max(3, steps // 8))
+    ms_s = graph_time(lambda: fused_swiglu(gate, up), 16, max(3, steps // 8))
+    ms_se = graph_time(lambda: F.silu(gate) * up, 16, max(3, steps // 8))
+    nb, sb = 3 * x.numel() * 2, 3 * gate.numel() * 2
+    return {"workload": "256-token decode step, Llama-3-8B: RMSNorm(x + residual) [256, 4096], "
+                        "SwiGLU [256, 14336], bf16",
+            "rmsnorm_us": round(ms_n * 1e3, 2), "rmsnorm_eager_us": round(ms_ne * 1e3, 2),
+            "rmsnorm_GBps": round(nb / (ms_n * 1e-3) / 1e9, 1),
+            "swiglu_us": round(ms_s * 1e3, 2), "swiglu_eager_us": round(ms_se * 1e3, 2),
+            "swiglu_GBps": round(sb / (ms_s * 1e-3) / 1e9, 1)}
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -371,6 +405,9 @@ def main() -> int:
         return 0
     if args.only == "block_copy":  # profiling aid: the page-copy section alone
         print(json.dumps({"block_copy": block_copy_section(dev, args.steps, args.warmup)}), flush=True)
+        return 0
+    if args.only == "norm_act":  # profiling aid: the RMSNorm / SwiGLU section alone
+        print(json.dumps({"norm_act": norm_act_section(dev, args.steps, args.warmup)}), flush=True)
         return 0
     if args.only == "rope_cache":  # profiling aid: the fused RoPE + scatter section alone
         print(json.dumps({"rope_cache": rope_cache_section(dev, args.steps, args.warmup)}), flush=True)
@@ -517,6 +554,9 @@ def main() -> int:
 
         # ---- fused RoPE + scatter ---------------------------------------------------
         result["rope_cache"] = rope_cache_section(dev, args.steps, args.warmup)
+
+        # ---- RMSNorm / SwiGLU ---------------------------------------------------------
+        result["norm_act"] = norm_act_section(dev, args.steps, args.warmup)
 
     if not args.no_cpu_baseline:
         b = workloads.llama_decode(device=dev, seed=args.seed)

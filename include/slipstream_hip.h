@@ -224,6 +224,27 @@ int ss_build_step_metadata(const int32_t* block_tables, int64_t bt_stride, int m
                            int block_size, int32_t* cu_seqlens, int32_t* context_lens,
                            int64_t* slot_mapping, int64_t total_tokens, void* stream);
 
+/*
+ * RMSNorm with an optional residual add: replaces fused_rmsnorm
+ * (slipstream/kernels/fused_rmsnorm.py:125-137) with the eager path's rounding
+ * (rmsnorm.py:30-33, fused_rmsnorm.py:73-82): s = x + residual in dtype,
+ * out = weight * dtype(s * rsqrt(mean(s^2) + eps)) with the variance in fp32.
+ * x, residual (or NULL), out: [rows, cols] with row strides in elements; weight
+ * [cols]. 16-byte aligned rows, cols a multiple of 8 (16-bit) or 4 (fp32), at
+ * most 16384 (16-bit) columns; otherwise SS_ERR_UNSUPPORTED.
+ */
+int ss_rmsnorm(const void* x, const void* residual, const void* weight, void* out, int64_t rows, int cols,
+               int64_t x_stride, int64_t r_stride, int64_t o_stride, float eps, int dtype, void* stream);
+
+/*
+ * SwiGLU: out = silu(gate) * up with the eager path's rounding (silu rounded to
+ * dtype, then the product): replaces fused_swiglu (slipstream/kernels/fused_swiglu.py:72-79)
+ * as MLP.forward runs it (slipstream/models/layers/mlp.py:37-40). [rows, cols], row
+ * strides in elements, 16-byte aligned rows, cols a multiple of 8 (16-bit) or 4.
+ */
+int ss_swiglu(const void* gate, const void* up, void* out, int64_t rows, int cols, int64_t g_stride,
+              int64_t u_stride, int64_t o_stride, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "ss_copy_blocks": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
     "ss_build_step_metadata": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _i64, _vp]),
+    "ss_rmsnorm": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, ctypes.c_float, _i32, _vp]),
+    "ss_swiglu": (_i32, [_vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _i32, _vp]),
     "ss_rope_and_cache": (
         _i32,
         [

@@ -7,6 +7,7 @@ from slipstream_amd.kernels.paged_attention import (
     paged_attention_prefill,
     paged_attention_varlen,
 )
+from slipstream_amd.kernels.norm_act import fused_rmsnorm, fused_swiglu
 from slipstream_amd.kernels.packed_step import packed_attention
 from slipstream_amd.kernels.quant_gemm import w4a16_gemm
 from slipstream_amd.kernels.reshape_and_cache import reshape_and_cache
@@ -14,6 +15,8 @@ from slipstream_amd.kernels.rope_cache import rope_and_cache
 
 __all__ = [
     "copy_blocks",
+    "fused_rmsnorm",
+    "fused_swiglu",
     "packed_attention",
     "paged_attention",
     "paged_attention_decode",

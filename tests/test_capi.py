@@ -24,7 +24,7 @@ def test_header_declares_entry_points():
     for required in ("ss_reshape_and_cache", "ss_paged_attention", "ss_paged_attention_varlen",
                      "ss_paged_attention_workspace_size", "ss_status_string", "ss_last_error",
                      "ss_w4a16_gemm", "ss_w4a16_workspace_size", "ss_copy_blocks", "ss_rope_and_cache",
-                     "ss_build_step_metadata"):
+                     "ss_build_step_metadata", "ss_rmsnorm", "ss_swiglu"):
         assert required in names
 
 

@@ -1,0 +1,110 @@
+"""RMSNorm / SwiGLU kernels against the reference's eager arithmetic (torch ops on the
+device, rmsnorm.py:30-33, fused_rmsnorm.py:73-82, mlp.py:37-40), and the quantized SwiGLU
+MLP (W4A16 linears + fused SwiGLU) against a fp32 dequantise-then-matmul reference."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from slipstream_amd.kernels import fused_rmsnorm, fused_swiglu
+from slipstream_amd.quantized import W4A16Linear, W4A16MLP
+
+pytestmark = pytest.mark.gpu
+
+# bf16/fp16: one unit in the last place. fp32: the reference's own fused-kernel
+# tolerance (test_fused_kernels.py:19, 1e-5), since there the fp32 sum order and
+# rsqrt / exp differences are not hidden by a final rounding.
+ULP = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10, torch.float32: 1e-5}
+
+
+def _close_within_one_ulp(got: torch.Tensor, want: torch.Tensor, what: str) -> None:
+    """Equal, except where the reference's fp32 sum order / rsqrt / exp make the value
+    before the final rounding differ in its last bits: then one unit in the last place
+    (16-bit), and at least 99 % of the elements bit-identical."""
+    g, w = got.float(), want.float()
+    tol = ULP[got.dtype] * w.abs() + (1e-6 if got.dtype == torch.float32 else 1e-30)
+    bad = (g - w).abs() > tol
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements out of tolerance"
+    if got.dtype != torch.float32:
+        exact = (g == w).float().mean().item()
+        assert exact > 0.99, f"{what}: only {exact:.4f} of the elements bit-identical"
+
+
+def _eager_rmsnorm(x, w, residual, eps):
+    if residual is not None:
+        x = x + residual
+    x32 = x.float()
+    return w * (x32 * torch.rsqrt(x32.pow(2).mean(dim=-1, keepdim=True) + eps)).to(x.dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("shape", [(2, 7, 4096), (5, 896), (3, 16), (2, 14336)])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_rmsnorm_matches_eager(device, dtype, shape, with_residual):
+    if dtype == torch.float32 and shape[-1] > 8192:
+        pytest.skip("fp32 rows are capped at 8192 columns")
+    g = torch.Generator(device=device).manual_seed(shape[-1])
+    x = torch.randn(shape, generator=g, device=device).to(dtype)
+    w = (1 + 0.1 * torch.randn(shape[-1], generator=g, device=device)).to(dtype)
+    r = torch.randn(shape, generator=g, device=device).to(dtype) if with_residual else None
+    _close_within_one_ulp(fused_rmsnorm(x, w, r, 1e-6), _eager_rmsnorm(x, w, r, 1e-6), f"rmsnorm {shape} {dtype}")
+
+
+def test_rmsnorm_reference_test_shape(device):
+    """test_fused_kernels.py:13-19: x [2, 8, 16], unit weight, fp32 -- atol/rtol 1e-5."""
+    g = torch.Generator(device=device).manual_seed(0)
+    x = torch.randn(2, 8, 16, generator=g, device=device)
+    w = torch.ones(16, device=device)
+    torch.testing.assert_close(fused_rmsnorm(x, w, eps=1e-6), _eager_rmsnorm(x, w, None, 1e-6), atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("shape", [(3, 14336), (64, 4864), (1, 8)])
+def test_swiglu_matches_eager(device, dtype, shape):
+    g = torch.Generator(device=device).manual_seed(shape[0])
+    gate = (3 * torch.randn(shape, generator=g, device=device)).to(dtype)
+    up = torch.randn(shape, generator=g, device=device).to(dtype)
+    _close_within_one_ulp(fused_swiglu(gate, up), F.silu(gate) * up, f"swiglu {shape} {dtype}")
+
+
+def test_strided_rows(device):
+    """Row views of wider buffers (a fused gate/up projection's halves)."""
+    g = torch.Generator(device=device).manual_seed(3)
+    gu = torch.randn(6, 2 * 4096, generator=g, device=device).to(torch.bfloat16)
+    gate, up = gu[:, :4096], gu[:, 4096:]
+    _close_within_one_ulp(fused_swiglu(gate, up), F.silu(gate) * up, "swiglu strided")
+    w = torch.ones(4096, device=device, dtype=torch.bfloat16)
+    _close_within_one_ulp(fused_rmsnorm(gate, w), _eager_rmsnorm(gate, w, None, 1e-6), "rmsnorm strided")
+
+
+@pytest.mark.parametrize("m", [1, 16, 64])
+def test_quantized_mlp_matches_dense_dequant(device, m):
+    """Qwen2.5-0.5B MLP shape (896 -> 4864 -> 896), g = 128: the W4A16 MLP equals the
+    same quantized weights dequantised and run densely in fp32 (1e-2 relative)."""
+    torch.manual_seed(m)
+    hid, inter = 896, 4864
+    mlp = torch.nn.Module()
+    mlp.gate_proj = torch.nn.Linear(hid, inter, bias=False)
+    mlp.up_proj = torch.nn.Linear(hid, inter, bias=False)
+    mlp.down_proj = torch.nn.Linear(inter, hid, bias=False)
+    mlp = mlp.to(device=device, dtype=torch.bfloat16)
+    q = W4A16MLP.from_mlp(mlp, 128)
+    x = torch.randn(m, hid, device=device, dtype=torch.bfloat16)
+    y = q(x)
+
+    def deq(lin: W4A16Linear) -> torch.Tensor:
+        shifts = torch.arange(0, 32, 4, device=device)
+        nib = (lin.qweight.to(torch.int64)[..., None] >> shifts) & 15
+        qv = nib.reshape(lin.out_features, lin.in_features).float()
+        s = lin.scales.float().repeat_interleave(lin.group_size, dim=1)
+        z = lin.qzeros.float().repeat_interleave(lin.group_size, dim=1)
+        return (qv - z) * s
+
+    g = x.float() @ deq(q.gate_proj).T
+    u = x.float() @ deq(q.up_proj).T
+    h = (F.silu(g.to(torch.bfloat16)) * u.to(torch.bfloat16)).float()
+    ref = h @ deq(q.down_proj).T
+    rel = ((y.float() - ref).norm() / ref.norm()).item()
+    assert rel < 1e-2, rel

@@ -148,3 +148,20 @@ def test_faithful_dequant_matches_torch_chain_and_reference_path():
     exact = quant.w4a16_gemm(x.float().numpy(), qw, s16.astype(np.float64), z, g)
     rel = np.linalg.norm(y_ref.float().numpy() - exact) / np.linalg.norm(exact)
     assert rel < 1e-2
+
+
+def test_module_quantizer_equals_oracle_quantizer():
+    """slipstream_amd.quantized.quantize_weight (the load-time format producer) restates
+    quant_ref.py:72-100 with torch ops: identical to the pinned numpy oracle."""
+    import torch
+
+    from slipstream_amd.quantized import quantize_weight
+
+    g = torch.Generator().manual_seed(2)
+    for group in (32, 128):
+        w = torch.randn(48, 512, generator=g) * 0.05
+        w[3, :group] = 0.25  # a constant group: 0 joins its range
+        qw, s, z = quantize_weight(w, group)
+        rq, rs, rz = quant.quantize_w4a16(w.numpy(), group)
+        assert np.array_equal(qw.numpy(), rq) and np.array_equal(z.numpy(), rz)
+        assert np.array_equal(s.numpy(), rs.astype(np.float32))
