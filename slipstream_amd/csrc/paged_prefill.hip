@@ -342,20 +342,24 @@ __device__ __forceinline__ void wait_vm() {
 extern __shared__ __attribute__((aligned(1024))) char s_tile_stages[];
 
 // Work split: a workgroup covers 128 query rows of one (sequence, KV head) with
-// 8 waves; wave w owns rows 16w .. 16w+15 (one MFMA tile) against all 64 keys of
-// every tile. Waves 0-3 issue the K loads and waves 4-7 the V loads of 16-key
-// group w%4. Registers are capped at two waves per SIMD (256 per lane); wider
-// row tiles per wave (which would halve the LDS reads per row) do not fit that
-// budget at head_dim 128 and spill. The LDS (three K tiles, three V tiles) is
+// WAVES waves. With 8, wave w owns rows 16w .. 16w+15 (one MFMA tile) against
+// all 64 keys of every tile; waves 0-3 issue the K loads and waves 4-7 the V
+// loads of 16-key group w%4; registers are capped at two waves per SIMD (256 per
+// lane), and wider row tiles per wave do not fit that budget at head_dim 128.
+// With 4, wave w owns rows 32w .. 32w+31 (two MFMA tiles, half the LDS reads
+// per row) at one wave per SIMD and loads both planes of group w. The LDS (three K tiles, three V tiles) is
 // dynamic shared memory: a static size would make the compiler size registers
 // for the occupancy that size alone allows.
-template <typename T, int D>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_tile_kernel(const AttnParams p) {
+template <typename T, int D, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(WAVES / 4, WAVES / 4))) void prefill_tile_kernel(const AttnParams p) {
+  static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
   typedef TileCfg<T, D> C;
-  constexpr int NT = 1;              // 16-row MFMA tiles per wave
   constexpr int ROWS = 128;
-  constexpr int XS = 4;              // 16-key subtiles of a tile
-  constexpr int LPG = C::NI;         // DMA instructions per wave and load group
+  constexpr int NT = ROWS / (16 * WAVES);  // 16-row MFMA tiles per wave
+  constexpr int XS = 4;                    // 16-key subtiles of a tile
+  // DMA instructions per wave and load group: with 8 waves a wave loads one
+  // plane of its group, with 4 both
+  constexpr int LPG = WAVES == 8 ? C::NI : 2 * C::NI;
   // V ring first: the V reads' stage, row and d offsets then all fit the 16-bit
   // immediate offset of the LDS instructions (the K reads use per-lane bases)
   char* const vring = s_tile_stages;                  // V tile j in slot j % 3
@@ -393,7 +397,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const uint32_t qflip = p.scale_log2 < 0.f ? 0x80008000u : 0u;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int rr = row0 + wave * 16 + 16 * nt + n;
+    const int rr = row0 + wave * 16 * NT + 16 * nt + n;
     const bool ok = rr < R;
     const int j = ok ? rr / p.n_rep : 0;
     const int hq = h * p.n_rep + (ok ? rr - j * p.n_rep : 0);
@@ -411,7 +415,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // wait for them lands inside the pipelined loop
   wait_vm<0>();
   // smallest causal limit over the wave's rows (rows past R do not count)
-  const int wrow = min(row0 + wave * 16, R - 1);
+  const int wrow = min(row0 + wave * 16 * NT, R - 1);
   const int wave_lim = min(kvt, ctx - qlen + wrow / p.n_rep + 1);
 
   const int tok_bytes = (int)(p.c_so * (int64_t)sizeof(T));
@@ -615,9 +619,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // HOLES: the sequence's table has an absent entry below kv_end. Without one
   // (the common case, found by one scan up front) a wave reads only its own
   // group's entry per tile and no tile needs validity bits.
-  const bool k_loader = wave < 4, v_loader = wave >= 4;
+  const bool k_loader = WAVES == 4 || wave < 4, v_loader = WAVES == 4 || wave >= 4;
   bool bad = false;
-  for (int i = threadIdx.x; i * p.block_size < kv_end; i += 512) {
+  for (int i = threadIdx.x; i * p.block_size < kv_end; i += 64 * WAVES) {
     const int v = p.bt[(int64_t)b * p.bt_stride + i];
     bad |= v < 0 || v >= p.num_blocks;
   }
@@ -659,7 +663,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     f32x4 sa[NT][XS], sb[NT][XS], sc[NT][XS];
     // group 0 landed; groups 1 and 2 may be in flight (a V loader's first load is
     // in group 1, so it waits for the same count)
-    wait_vm<2 * C::NI>();
+    wait_vm<2 * LPG>();
     __syncthreads();
     qk(0, sa);
     // K slot of tile t+1 = (t+1) % 3, V slot of tile t = t % 3
@@ -695,7 +699,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const float lt = lsum[nt][0];
-    const int rr = row0 + wave * 16 + 16 * nt + n;
+    const int rr = row0 + wave * 16 * NT + 16 * nt + n;
     if (rr < R) {
       const int j = rr / p.n_rep;
       const int hq = h * p.n_rep + (rr - j * p.n_rep);
@@ -715,6 +719,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 constexpr int kPrefillNT = 2;
+// 8 waves of 16 rows at two waves per SIMD. The 4-wave form (32 rows per wave,
+// half the LDS reads, one wave per SIMD with up to 512 registers) measured
+// 189 us against 150 us for the C3 chunks: one wave per SIMD hides too little.
+constexpr int kTileWaves = 8;
 
 template <typename T, int D>
 int launch_prefill_typed(const AttnParams& p, int max_query_len, hipStream_t stream) {
@@ -731,14 +739,14 @@ int launch_prefill_typed(const AttnParams& p, int max_query_len, hipStream_t str
     const int lds = 6 * TileCfg<T, DD>::PLANE;
     static bool attr_set = false;  // per instantiation; the attribute is process-wide
     if (!attr_set) {
-      if (hipFuncSetAttribute((const void*)prefill_tile_kernel<T, DD>,
+      if (hipFuncSetAttribute((const void*)prefill_tile_kernel<T, DD, kTileWaves>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess) {
         ss_host::set_error("paged attention prefill: cannot reserve %d bytes of LDS", lds);
         return SS_ERR_UNSUPPORTED;
       }
       attr_set = true;
     }
-    hipLaunchKernelGGL((prefill_tile_kernel<T, DD>), dim3((unsigned)qtiles, p.n_kv, p.batch), dim3(512), lds,
+    hipLaunchKernelGGL((prefill_tile_kernel<T, DD, kTileWaves>), dim3((unsigned)qtiles, p.n_kv, p.batch), dim3(64 * kTileWaves), lds,
                        stream, p);
     return ss_host::launch_status("paged attention prefill");
   }
