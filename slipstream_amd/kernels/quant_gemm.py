@@ -20,7 +20,8 @@ import torch
 from slipstream_amd import _ffi
 from slipstream_amd.kernels._common import require_device
 
-# Arrival counters + split-K partials, one zero-initialised buffer per (device, stream).
+# Split-K partials of the tiled kernel, one buffer per (device, stream): every call writes
+# the partials it reads, so the buffer needs no initialisation and keeps no state.
 _WORKSPACE: dict[tuple[int, int], torch.Tensor] = {}
 
 
@@ -30,8 +31,7 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor |
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     ws = _WORKSPACE.get(key)
     if ws is None or ws.numel() < nbytes:
-        # zero-filled: the counters at its head must start at zero; calls leave them zero
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACE[key] = ws
     return ws
 

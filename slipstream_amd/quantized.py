@@ -6,8 +6,10 @@ int32 nibbles ``[N, K/8]``, scales ``[N, K/g]``, int32 zero points ``[N, K/g]``)
 (``slipstream/models/layers/mlp.py:12-40``, ``down(silu(gate(x)) * up(x))``) on three of
 them with ``fused_swiglu`` between. ``from_linear`` / ``from_mlp`` quantize dense
 modules once, at load, with the reference's quantizer (``quant_ref.py:72-100``,
-restated below with torch ops on the weight's device); the forward passes are the
-HIP kernels only.
+restated below with torch ops on the weight's device); ``from_awq`` / ``from_gptq`` /
+``from_state_dict`` re-lay out the tensors of AWQ and GPTQ checkpoints into the reference
+format at load (the quantized-model loading the reference plans, ``MASTERPLAN.md:620-627``).
+The forward passes are the HIP kernels only.
 """
 
 from __future__ import annotations
@@ -45,6 +47,86 @@ def quantize_weight(weight: torch.Tensor, group_size: int) -> tuple[torch.Tensor
     return qweight, scale.squeeze(-1).to(weight.dtype), zero.squeeze(-1).to(torch.int32)
 
 
+# AutoAWQ's GEMM layout packs eight output columns per int32 word in this order: nibble i
+# (bits 4i..4i+3) of word j holds column 8j + _AWQ_ORDER[i].
+_AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
+
+
+def _nibbles(words: torch.Tensor) -> torch.Tensor:
+    """int32 words [..., w] -> int64 nibbles [..., w, 8], nibble i = bits 4i..4i+3."""
+    if words.dtype != torch.int32:
+        raise ValueError(f"packed int4 tensors must be int32, got {words.dtype}")
+    shifts = torch.arange(0, 32, 4, device=words.device, dtype=torch.int64)
+    return (words.to(torch.int64).unsqueeze(-1) >> shifts) & 0xF
+
+
+def _pack_rows(q: torch.Tensor) -> torch.Tensor:
+    """int64 [N, K] values 0..15 -> the reference's int32 [N, K/8] (nibble n = q[8j+n])."""
+    n, k = q.shape
+    shifts = torch.arange(0, 32, 4, device=q.device, dtype=torch.int64)
+    return (q.view(n, k // 8, 8) << shifts).sum(dim=-1).to(torch.int32)
+
+
+def _check_group_layout(k: int, n: int, scales: torch.Tensor, group_size: int, who: str) -> None:
+    if group_size <= 0 or group_size % 8 or k % group_size:
+        raise ValueError(f"{who}: group_size {group_size} must be a multiple of 8 dividing in_features {k}")
+    if tuple(scales.shape) != (k // group_size, n):
+        raise ValueError(f"{who}: scales {tuple(scales.shape)} != [in/group_size={k // group_size}, out={n}]")
+
+
+def awq_to_reference(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
+                     group_size: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """AutoAWQ GEMM checkpoint tensors -> the reference format (``quant_ref.py:8-20``).
+
+    AWQ stores ``qweight`` int32 ``[in, out/8]`` and ``qzeros`` int32 ``[in/g, out/8]``
+    with eight output columns per word in the order of ``_AWQ_ORDER``, and ``scales``
+    ``[in/g, out]``; the weight is ``W[o, i] = (q[i, o] - z[i/g, o]) * s[i/g, o]``, the
+    reference's affine form. Returns ``(qweight [out, in/8], scales [out, in/g],
+    qzeros [out, in/g])``, a pure re-layout (the dequantised weight is unchanged)."""
+    if qweight.ndim != 2 or qzeros.ndim != 2 or scales.ndim != 2:
+        raise ValueError("awq: qweight, qzeros and scales must be 2-D")
+    k, n = qweight.shape[0], qweight.shape[1] * 8
+    _check_group_layout(k, n, scales, group_size, "awq")
+    if tuple(qzeros.shape) != (k // group_size, n // 8):
+        raise ValueError(f"awq: qzeros {tuple(qzeros.shape)} != [in/group_size, out/8]")
+    inv = torch.tensor(_AWQ_ORDER, device=qweight.device).argsort()  # column c%8 -> nibble
+    q = _nibbles(qweight)[..., inv].reshape(k, n)
+    z = _nibbles(qzeros)[..., inv.to(qzeros.device)].reshape(k // group_size, n)
+    return _pack_rows(q.t().contiguous()), scales.t().contiguous(), z.t().contiguous().to(torch.int32)
+
+
+def gptq_to_reference(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor, group_size: int,
+                      g_idx: torch.Tensor | None = None,
+                      checkpoint_format: str = "gptq") -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """GPTQ checkpoint tensors (AutoGPTQ / GPTQModel layout) -> the reference format.
+
+    GPTQ stores ``qweight`` int32 ``[in/8, out]`` (nibble i of word ``[j, o]`` is input
+    row 8j+i), ``qzeros`` int32 ``[in/g, out/8]`` (nibble i of word ``[r, j]`` is output
+    column 8j+i), ``scales`` ``[in/g, out]`` and ``g_idx`` (each input row's group). The
+    ``"gptq"`` (v1) format stores each zero point minus one and its dequantisation adds
+    the one back (``z = stored + 1``, so a stored 15 means 16); ``"gptq_v2"`` stores the
+    zero point itself. Checkpoints quantized with act-order (``g_idx`` other than
+    ``i // group_size``) group inputs out of order, which the reference format cannot
+    express: they raise ``ValueError``."""
+    if checkpoint_format not in ("gptq", "gptq_v2"):
+        raise ValueError(f"gptq: checkpoint_format must be 'gptq' or 'gptq_v2', got {checkpoint_format!r}")
+    if qweight.ndim != 2 or qzeros.ndim != 2 or scales.ndim != 2:
+        raise ValueError("gptq: qweight, qzeros and scales must be 2-D")
+    k, n = qweight.shape[0] * 8, qweight.shape[1]
+    _check_group_layout(k, n, scales, group_size, "gptq")
+    if tuple(qzeros.shape) != (k // group_size, n // 8):
+        raise ValueError(f"gptq: qzeros {tuple(qzeros.shape)} != [in/group_size, out/8]")
+    if g_idx is not None:
+        want = torch.arange(k, device=g_idx.device, dtype=torch.int64) // group_size
+        if g_idx.numel() != k or not torch.equal(g_idx.reshape(-1).to(torch.int64), want):
+            raise ValueError("gptq: act-order g_idx (inputs grouped out of order) is not supported")
+    q = _nibbles(qweight).permute(0, 2, 1).reshape(k, n)  # [in/8, out, 8] -> rows 8j+i
+    z = _nibbles(qzeros).reshape(k // group_size, n)
+    if checkpoint_format == "gptq":
+        z = z + 1
+    return _pack_rows(q.t().contiguous()), scales.t().contiguous(), z.t().contiguous().to(torch.int32)
+
+
 class W4A16Linear(nn.Module):
     """``y = x @ dequant(W).T (+ bias)`` through ``w4a16_gemm``."""
 
@@ -64,6 +146,36 @@ class W4A16Linear(nn.Module):
         qweight, scales, qzeros = quantize_weight(linear.weight.detach(), group_size)
         bias = linear.bias.detach().clone() if linear.bias is not None else None
         return cls(qweight, scales, qzeros, group_size, bias)
+
+    @classmethod
+    def from_awq(cls, qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor, group_size: int,
+                 bias: torch.Tensor | None = None) -> "W4A16Linear":
+        """From the tensors of an AutoAWQ GEMM checkpoint (``awq_to_reference``)."""
+        return cls(*awq_to_reference(qweight, qzeros, scales, group_size), group_size, bias)
+
+    @classmethod
+    def from_gptq(cls, qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor, group_size: int,
+                  g_idx: torch.Tensor | None = None, bias: torch.Tensor | None = None,
+                  checkpoint_format: str = "gptq") -> "W4A16Linear":
+        """From the tensors of a GPTQ checkpoint (``gptq_to_reference``)."""
+        return cls(*gptq_to_reference(qweight, qzeros, scales, group_size, g_idx, checkpoint_format),
+                   group_size, bias)
+
+    @classmethod
+    def from_state_dict(cls, state: dict, prefix: str, group_size: int, checkpoint_format: str = "awq",
+                        device: torch.device | str | None = None) -> "W4A16Linear":
+        """Load ``prefix.{qweight,qzeros,scales[,g_idx][,bias]}`` from a checkpoint's tensors
+        (e.g. ``safetensors.torch.load_file``); ``checkpoint_format`` is ``"awq"``, ``"gptq"``
+        or ``"gptq_v2"``."""
+        def get(name: str, required: bool = True):
+            t = state.get(f"{prefix}.{name}")
+            if t is None and required:
+                raise KeyError(f"{prefix}.{name} missing from the checkpoint")
+            return t if t is None or device is None else t.to(device)
+        if checkpoint_format == "awq":
+            return cls.from_awq(get("qweight"), get("qzeros"), get("scales"), group_size, get("bias", False))
+        return cls.from_gptq(get("qweight"), get("qzeros"), get("scales"), group_size, get("g_idx", False),
+                             get("bias", False), checkpoint_format)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         y = w4a16_gemm(x, self.qweight, self.scales, self.qzeros, self.group_size)
@@ -89,6 +201,13 @@ class W4A16MLP(nn.Module):
         return cls(W4A16Linear.from_linear(mlp.gate_proj, group_size),
                    W4A16Linear.from_linear(mlp.up_proj, group_size),
                    W4A16Linear.from_linear(mlp.down_proj, group_size))
+
+    @classmethod
+    def from_state_dict(cls, state: dict, prefix: str, group_size: int, checkpoint_format: str = "awq",
+                        device: torch.device | str | None = None) -> "W4A16MLP":
+        """Load ``prefix.{gate,up,down}_proj`` quantized linears from a checkpoint's tensors."""
+        return cls(*(W4A16Linear.from_state_dict(state, f"{prefix}.{name}", group_size, checkpoint_format, device)
+                     for name in ("gate_proj", "up_proj", "down_proj")))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self.down_proj(fused_swiglu(self.gate_proj(x), self.up_proj(x)))

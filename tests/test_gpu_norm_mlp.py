@@ -108,3 +108,39 @@ def test_quantized_mlp_matches_dense_dequant(device, m):
     ref = h @ deq(q.down_proj).T
     rel = ((y.float() - ref).norm() / ref.norm()).item()
     assert rel < 1e-2, rel
+
+
+@pytest.mark.parametrize("fmt", ["awq", "gptq"])
+def test_checkpoint_linear_matches_checkpoint_weight(device, fmt):
+    """A linear loaded from AWQ / GPTQ tensors (4096 -> 1024, g = 128, every zero point
+    0..15, so GPTQ v1 also reads 16) equals x @ W.T with the weight the checkpoint
+    describes, W[o, i] = (q[i, o] - z[i/g, o]) * s[i/g, o], in fp32 (1e-2 relative)."""
+    from slipstream_amd.quantized import _AWQ_ORDER
+    k, n, g, m = 4096, 1024, 128, 16
+    gen = torch.Generator().manual_seed(7)
+    q = torch.randint(0, 16, (k, n), generator=gen)
+    z = torch.randint(0, 16, (k // g, n), generator=gen)
+    s = (torch.rand(k // g, n, generator=gen) * 0.015 + 0.005).half()
+    shifts = torch.arange(0, 32, 4)
+
+    def pack(v: torch.Tensor) -> torch.Tensor:  # [..., 8] nibbles -> int32 words
+        return ((v & 15) << shifts).sum(-1).to(torch.int64).sub(
+            ((v & 15) << shifts).sum(-1).ge(1 << 31).to(torch.int64) << 32).to(torch.int32)
+
+    if fmt == "awq":
+        order = torch.tensor(_AWQ_ORDER)
+        state = {"p.qweight": pack(q.view(k, n // 8, 8)[..., order]),
+                 "p.qzeros": pack(z.view(k // g, n // 8, 8)[..., order]), "p.scales": s}
+        zt = z
+    else:
+        state = {"p.qweight": pack(q.view(k // 8, 8, n).permute(0, 2, 1)),
+                 "p.qzeros": pack((z - 1).view(k // g, n // 8, 8)), "p.scales": s,
+                 "p.g_idx": torch.arange(k, dtype=torch.int32) // g}
+        zt = torch.where(z == 0, torch.full_like(z, 16), z)  # v1: stored z-1, read back + 1
+    lin = W4A16Linear.from_state_dict(state, "p", g, fmt, device=device)
+    w = ((q - zt.repeat_interleave(g, 0)).float() * s.float().repeat_interleave(g, 0)).T.to(device)
+    x = torch.randn(m, k, device=device, dtype=torch.bfloat16)
+    ref = x.float() @ w.T
+    y = lin(x)
+    rel = ((y.float() - ref).norm() / ref.norm()).item()
+    assert rel < 1e-2, rel
