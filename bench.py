@@ -215,7 +215,8 @@ def w4a16_section(dev, steps: int, warmup: int) -> dict:
 
     cases = []
     layer_us = {}
-    for k, n, name in C5_SHAPES:
+    fused_us = {}  # the quantized MLP's layout: gate and up as one 4096 x 28672 linear
+    for k, n, name in C5_SHAPES + [(4096, 2 * 14336, "gate_up")]:
         if name == "up":  # same shape as gate: timed once, counted twice in the layer total
             continue
         base = workloads.w4a16_linear(k, n, 256, device=dev, seed=k + n)
@@ -243,12 +244,18 @@ def w4a16_section(dev, steps: int, warmup: int) -> dict:
             cases.append({"linear": name, "k": k, "n": n, "m": m, "us": round(ms * 1e3, 2), "GBps": round(gbs, 1),
                           "TFLOPs": round(tfl, 2), "bound": bound, "frac": round(frac, 4),
                           "weight_copies": copies})
-            layer_us[m] = layer_us.get(m, 0.0) + ms * 1e3 * (2 if name == "gate" else 1)
+            if name != "gate_up":
+                layer_us[m] = layer_us.get(m, 0.0) + ms * 1e3 * (2 if name == "gate" else 1)
+            if name != "gate":
+                fused_us[m] = fused_us.get(m, 0.0) + ms * 1e3
         del qws, scs, qzs, base
         torch.cuda.empty_cache()
     return {"workload": "C5 W4A16 linears of one Llama-3-8B layer (qkv 4096x6144, o 4096x4096, gate/up "
                         "4096x14336, down 14336x4096), g=128, fp16 scales, zeros 8, bf16 x",
-            "cases": cases, "layer_us_by_m": {str(m): round(v, 2) for m, v in layer_us.items()}}
+            "cases": cases, "layer_us_by_m": {str(m): round(v, 2) for m, v in layer_us.items()},
+            "layer_fused_gate_up_us_by_m": {str(m): round(v, 2) for m, v in fused_us.items()},
+            "note": "layer = qkv + o + gate + up + down (the reference's linears); layer_fused_gate_up = "
+                    "qkv + o + gate_up + down (W4A16MLP's layout: gate and up stacked in one launch)"}
 
 
 def block_copy_section(dev, steps: int, warmup: int) -> dict:

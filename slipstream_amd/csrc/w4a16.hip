@@ -890,8 +890,10 @@ struct W4Plan {
 // m > 64 (MFMA-bound) takes 64 x 64 wave tiles. The K split aims at two
 // workgroups per CU (one for m > 64), each range at least one round of PF stages,
 // with the workgroup's scale table within kTileTableMax bytes of LDS; the
-// partials take ks * m * n floats of workspace.
-constexpr int kTileTableMax = 64 * 1024;
+// partials take ks * m * n floats of workspace. The cap keeps two workgroups per
+// CU: with the 35 KB activation stages of m > 32, a 64 KB table left room for one
+// (a 4096 x 28672 linear at m = 256 took 233 us instead of 2 x 67 us).
+constexpr int kTileTableMax = 40 * 1024;
 
 size_t tile_table_bytes(int ns, int kchunk, int g) {
   const int gr = (kchunk * 128 + g - 1) / g + 1;  // groups a range can touch
@@ -923,8 +925,12 @@ bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
   int64_t ks = (target + tiles - 1) / tiles;
   ks = ks < 1 ? 1 : (ks > rounds ? rounds : ks);
   if (ks > 65535) return false;
+  // more ranges while a range's scale table is too large; the ranges stay balanced
   int64_t per = (rounds + ks - 1) / ks;
-  while (per > 1 && tile_table_bytes(ns, (int)(per * pf), g) > (size_t)kTileTableMax) --per;
+  while (per > 1 && tile_table_bytes(ns, (int)(per * pf), g) > (size_t)kTileTableMax) {
+    ++ks;
+    per = (rounds + ks - 1) / ks;
+  }
   if (tile_table_bytes(ns, (int)(per * pf), g) > (size_t)kTileTableMax) return false;
   pl.tile = true;
   pl.mt = mt, pl.ns = ns, pl.pf = pf;

@@ -186,12 +186,29 @@ class W4A16Linear(nn.Module):
 
 
 class W4A16MLP(nn.Module):
-    """SwiGLU MLP (``mlp.py:12-40``) on W4A16 linears: ``down(silu(gate(x)) * up(x))``."""
+    """SwiGLU MLP (``mlp.py:12-40``) on W4A16 linears: ``down(silu(gate(x)) * up(x))``.
+
+    The gate and up projections are held as one linear of ``2 * intermediate`` output
+    rows (gate rows first): both read the same ``x``, so one launch streams both weights
+    and stages ``x`` once, and ``fused_swiglu`` reads the two halves of its output in
+    place. Quantization is per output row, so the fused weight is exactly the two
+    weights stacked.
+    """
 
     def __init__(self, gate_proj: W4A16Linear, up_proj: W4A16Linear, down_proj: W4A16Linear) -> None:
         super().__init__()
-        self.gate_proj = gate_proj
-        self.up_proj = up_proj
+        if (gate_proj.in_features, gate_proj.out_features, gate_proj.group_size) != (
+                up_proj.in_features, up_proj.out_features, up_proj.group_size):
+            raise ValueError("gate_proj and up_proj must share in/out features and group size")
+        bias = None
+        if gate_proj.bias is not None or up_proj.bias is not None:
+            zeros = lambda lin: torch.zeros(lin.out_features, dtype=lin.scales.dtype, device=lin.scales.device)
+            bias = torch.cat([gate_proj.bias if gate_proj.bias is not None else zeros(gate_proj),
+                              up_proj.bias if up_proj.bias is not None else zeros(up_proj)])
+        self.intermediate = gate_proj.out_features
+        self.gate_up_proj = W4A16Linear(torch.cat([gate_proj.qweight, up_proj.qweight]),
+                                        torch.cat([gate_proj.scales, up_proj.scales]),
+                                        torch.cat([gate_proj.qzeros, up_proj.qzeros]), gate_proj.group_size, bias)
         self.down_proj = down_proj
 
     @classmethod
@@ -210,4 +227,6 @@ class W4A16MLP(nn.Module):
                      for name in ("gate_proj", "up_proj", "down_proj")))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.down_proj(fused_swiglu(self.gate_proj(x), self.up_proj(x)))
+        gu = self.gate_up_proj(x)
+        i = self.intermediate
+        return self.down_proj(fused_swiglu(gu[..., :i], gu[..., i:]))

@@ -81,8 +81,9 @@ def test_strided_rows(device):
 
 @pytest.mark.parametrize("m", [1, 16, 64])
 def test_quantized_mlp_matches_dense_dequant(device, m):
-    """Qwen2.5-0.5B MLP shape (896 -> 4864 -> 896), g = 128: the W4A16 MLP equals the
-    same quantized weights dequantised and run densely in fp32 (1e-2 relative)."""
+    """Qwen2.5-0.5B MLP shape (896 -> 4864 -> 896), g = 128: the W4A16 MLP (gate and up
+    fused into one launch) equals the separately quantized gate / up / down weights
+    dequantised and run densely in fp32 (1e-2 relative)."""
     torch.manual_seed(m)
     hid, inter = 896, 4864
     mlp = torch.nn.Module()
@@ -91,6 +92,7 @@ def test_quantized_mlp_matches_dense_dequant(device, m):
     mlp.down_proj = torch.nn.Linear(inter, hid, bias=False)
     mlp = mlp.to(device=device, dtype=torch.bfloat16)
     q = W4A16MLP.from_mlp(mlp, 128)
+    parts = [W4A16Linear.from_linear(lin, 128) for lin in (mlp.gate_proj, mlp.up_proj, mlp.down_proj)]
     x = torch.randn(m, hid, device=device, dtype=torch.bfloat16)
     y = q(x)
 
@@ -102,10 +104,10 @@ def test_quantized_mlp_matches_dense_dequant(device, m):
         z = lin.qzeros.float().repeat_interleave(lin.group_size, dim=1)
         return (qv - z) * s
 
-    g = x.float() @ deq(q.gate_proj).T
-    u = x.float() @ deq(q.up_proj).T
+    g = x.float() @ deq(parts[0]).T
+    u = x.float() @ deq(parts[1]).T
     h = (F.silu(g.to(torch.bfloat16)) * u.to(torch.bfloat16)).float()
-    ref = h @ deq(q.down_proj).T
+    ref = h @ deq(parts[2]).T
     rel = ((y.float() - ref).norm() / ref.norm()).item()
     assert rel < 1e-2, rel
 

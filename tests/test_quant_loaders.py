@@ -131,7 +131,12 @@ def test_state_dict_loader_builds_modules():
         state[f"model.layers.0.mlp.{name}.qzeros"] = awq_pack(z)
         state[f"model.layers.0.mlp.{name}.scales"] = s
     mlp = W4A16MLP.from_state_dict(state, "model.layers.0.mlp", g)
-    assert (mlp.gate_proj.in_features, mlp.gate_proj.out_features) == (k, n)
+    assert (mlp.gate_up_proj.in_features, mlp.gate_up_proj.out_features, mlp.intermediate) == (k, 2 * n, n)
+    gate = W4A16Linear.from_state_dict(state, "model.layers.0.mlp.gate_proj", g)
+    up = W4A16Linear.from_state_dict(state, "model.layers.0.mlp.up_proj", g)
+    assert torch.equal(mlp.gate_up_proj.qweight, torch.cat([gate.qweight, up.qweight]))
+    assert torch.equal(mlp.gate_up_proj.qzeros, torch.cat([gate.qzeros, up.qzeros]))
+    assert torch.equal(mlp.gate_up_proj.scales, torch.cat([gate.scales, up.scales]))
     assert (mlp.down_proj.in_features, mlp.down_proj.out_features) == (n * 8, k)
     with pytest.raises(KeyError, match="qzeros"):
         W4A16Linear.from_state_dict({"x.qweight": state["model.layers.0.mlp.gate_proj.qweight"]}, "x", g)
