@@ -668,17 +668,37 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const AttnParams p, i
       const int slot = i == 0 ? slot0 : 0;
       return (((int64_t)(wr * p.n_hgroups + hg) * 2 + slot) * p.hpw + wave) * p.rmax + r;
     };
-    float mmax = kNegBig;
-    for (int i = 0; i < np; ++i) mmax = fmaxf(mmax, p.ws_ml[piece(i) * 2]);
-    float lsum = 0.f;
+    // pieces four at a time: every load of a batch is issued before any is used (one
+    // memory round trip per batch), then merged into the running (max, sum, output)
+    float mmax = kNegBig, lsum = 0.f;
     f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
-    for (int i = 0; i < np; ++i) {
-      const int64_t pi = piece(i);
-      const float f = fast_exp2(p.ws_ml[pi * 2] - mmax);
-      lsum += p.ws_ml[pi * 2 + 1] * f;
-      const f32x4* po = reinterpret_cast<const f32x4*>(p.ws_o + pi * D + 8 * c);
-      o0 += po[0] * f;
-      o1 += po[1] * f;
+    for (int i0 = 0; i0 < np; i0 += 4) {
+      float mv[4], lv[4];
+      f32x4 a0[4], a1[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t pi = piece(min(i0 + j, np - 1));
+        mv[j] = p.ws_ml[pi * 2];
+        lv[j] = p.ws_ml[pi * 2 + 1];
+        const f32x4* po = reinterpret_cast<const f32x4*>(p.ws_o + pi * D + 8 * c);
+        a0[j] = po[0];
+        a1[j] = po[1];
+      }
+      float mx = mmax;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) mx = i0 + j < np ? fmaxf(mx, mv[j]) : mx;
+      const float keep = fast_exp2(mmax - mx);
+      lsum *= keep;
+      o0 *= keep;
+      o1 *= keep;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float f = i0 + j < np ? fast_exp2(mv[j] - mx) : 0.f;
+        lsum += lv[j] * f;
+        o0 += a0[j] * f;
+        o1 += a1[j] * f;
+      }
+      mmax = mx;
     }
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
     const int j = r / p.n_rep;
