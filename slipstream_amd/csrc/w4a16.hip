@@ -23,7 +23,7 @@
 // order. There is no synchronisation between workgroups.
 //
 // Tiled kernel (w4a16_tile_kernel, m >= 2 and g % 128 == 0; m <= 16 only for
-// K >= 8192): four waves split 64*NS weight rows and share the activation tile
+// K >= 8192 or N >= 24576): four waves split 64*NS weight rows and share the activation tile
 // through LDS; K is split over workgroups and a second kernel adds the fp32
 // partials in range order. Batch 1 takes a bandwidth GEMV. In every case the
 // result does not depend on timing.
@@ -903,8 +903,10 @@ size_t tile_table_bytes(int ns, int kchunk, int g) {
 bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
   if (!pl.wide || m < 2) return false;
   // m <= 16 is weight-bandwidth bound and the untiled kernel shares activations
-  // well enough there; for K < 8192 it measured faster (no reduction launch)
-  if (m <= 16 && k < 8192) return false;
+  // well enough there; for K < 8192 it measured faster (no reduction launch) up to
+  // N = 14336 (11.5 vs 12.8 us at 4096 x 6144), the tiled one from N = 28672 (26.9 vs
+  // 30.9 us at 4096 x 28672, the stacked gate/up projection)
+  if (m <= 16 && k < 8192 && n < 24576) return false;
   int mt, ns, pf;
   if (m <= 16)
     mt = 1, ns = 2, pf = 8;

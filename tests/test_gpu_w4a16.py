@@ -120,6 +120,7 @@ def test_batch1_gemv_strided_activation(device):
     (100, 4096, 1000, 256, torch.bfloat16, torch.float32),   # 64x64 wave tiles, a partial second M block
     (24, 8192, 3000, 512, torch.float16, torch.float16),     # 32-row activation tiles
     (9, 8192, 700, 128, torch.bfloat16, torch.bfloat16),     # m <= 16 at K >= 8192 takes the tiled kernel
+    (16, 1024, 24600, 128, torch.bfloat16, torch.float16),   # m <= 16 at N >= 24576 takes it too
 ])
 def test_tiled_split_k(device, m, k, n, g, act, sdt):
     """The tiled kernel (activations shared through LDS, K split over workgroups with
@@ -211,7 +212,8 @@ def test_argument_errors(device):
     assert w4a16_gemm(x[:0], qw, s, z, 128).shape == (0, 8)
 
 
-C5_SHAPES = [(4096, 6144, "qkv"), (4096, 4096, "o"), (4096, 14336, "gate/up"), (14336, 4096, "down")]
+C5_SHAPES = [(4096, 6144, "qkv"), (4096, 4096, "o"), (4096, 14336, "gate/up"), (14336, 4096, "down"),
+             (4096, 28672, "gate_up stacked")]
 
 
 @pytest.mark.parametrize("k,n,name", C5_SHAPES)
