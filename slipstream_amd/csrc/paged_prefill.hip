@@ -342,24 +342,22 @@ __device__ __forceinline__ void wait_vm() {
 extern __shared__ __attribute__((aligned(1024))) char s_tile_stages[];
 
 // Work split: a workgroup covers 128 query rows of one (sequence, KV head) with
-// WAVES waves. With 8, wave w owns rows 16w .. 16w+15 (one MFMA tile) against
-// all 64 keys of every tile; waves 0-3 issue the K loads and waves 4-7 the V
-// loads of 16-key group w%4; registers are capped at two waves per SIMD (256 per
-// lane), and wider row tiles per wave do not fit that budget at head_dim 128.
-// With 4, wave w owns rows 32w .. 32w+31 (two MFMA tiles, half the LDS reads
-// per row) at one wave per SIMD and loads both planes of group w. The LDS (three K tiles, three V tiles) is
+// 8 waves; wave w owns rows 16w .. 16w+15 (one MFMA tile) against all 64 keys of
+// every tile. Waves 0-3 issue the K loads and waves 4-7 the V loads of 16-key
+// group w%4. Registers are capped at two waves per SIMD (256 per lane); wider
+// row tiles per wave (which would halve the LDS reads per row) do not fit that
+// budget at head_dim 128, and at one wave per SIMD (up to 512 registers: 4 waves
+// of 32 rows) the kernel measured slower (189 vs 150 us on the C3 chunks): one
+// wave per SIMD hides too little. The LDS (three K tiles, three V tiles) is
 // dynamic shared memory: a static size would make the compiler size registers
 // for the occupancy that size alone allows.
-template <typename T, int D, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(WAVES / 4, WAVES / 4))) void prefill_tile_kernel(const AttnParams p) {
-  static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
+template <typename T, int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_tile_kernel(const AttnParams p) {
   typedef TileCfg<T, D> C;
+  constexpr int NT = 1;              // 16-row MFMA tiles per wave
   constexpr int ROWS = 128;
-  constexpr int NT = ROWS / (16 * WAVES);  // 16-row MFMA tiles per wave
-  constexpr int XS = 4;                    // 16-key subtiles of a tile
-  // DMA instructions per wave and load group: with 8 waves a wave loads one
-  // plane of its group, with 4 both
-  constexpr int LPG = WAVES == 8 ? C::NI : 2 * C::NI;
+  constexpr int XS = 4;              // 16-key subtiles of a tile
+  constexpr int LPG = C::NI;         // DMA instructions per wave and load group
   // V ring first: the V reads' stage, row and d offsets then all fit the 16-bit
   // immediate offset of the LDS instructions (the K reads use per-lane bases)
   char* const vring = s_tile_stages;                  // V tile j in slot j % 3
@@ -619,9 +617,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(WAVE
   // HOLES: the sequence's table has an absent entry below kv_end. Without one
   // (the common case, found by one scan up front) a wave reads only its own
   // group's entry per tile and no tile needs validity bits.
-  const bool k_loader = WAVES == 4 || wave < 4, v_loader = WAVES == 4 || wave >= 4;
+  const bool k_loader = wave < 4, v_loader = wave >= 4;
   bool bad = false;
-  for (int i = threadIdx.x; i * p.block_size < kv_end; i += 64 * WAVES) {
+  for (int i = threadIdx.x; i * p.block_size < kv_end; i += 512) {
     const int v = p.bt[(int64_t)b * p.bt_stride + i];
     bad |= v < 0 || v >= p.num_blocks;
   }
@@ -719,10 +717,6 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(WAVE
 }
 
 constexpr int kPrefillNT = 2;
-// 8 waves of 16 rows at two waves per SIMD. The 4-wave form (32 rows per wave,
-// half the LDS reads, one wave per SIMD with up to 512 registers) measured
-// 189 us against 150 us for the C3 chunks: one wave per SIMD hides too little.
-constexpr int kTileWaves = 8;
 
 template <typename T, int D>
 int launch_prefill_typed(const AttnParams& p, int max_query_len, hipStream_t stream) {
@@ -739,14 +733,14 @@ int launch_prefill_typed(const AttnParams& p, int max_query_len, hipStream_t str
     const int lds = 6 * TileCfg<T, DD>::PLANE;
     static bool attr_set = false;  // per instantiation; the attribute is process-wide
     if (!attr_set) {
-      if (hipFuncSetAttribute((const void*)prefill_tile_kernel<T, DD, kTileWaves>,
+      if (hipFuncSetAttribute((const void*)prefill_tile_kernel<T, DD>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess) {
         ss_host::set_error("paged attention prefill: cannot reserve %d bytes of LDS", lds);
         return SS_ERR_UNSUPPORTED;
       }
       attr_set = true;
     }
-    hipLaunchKernelGGL((prefill_tile_kernel<T, DD, kTileWaves>), dim3((unsigned)qtiles, p.n_kv, p.batch), dim3(64 * kTileWaves), lds,
+    hipLaunchKernelGGL((prefill_tile_kernel<T, DD>), dim3((unsigned)qtiles, p.n_kv, p.batch), dim3(512), lds,
                        stream, p);
     return ss_host::launch_status("paged attention prefill");
   }
