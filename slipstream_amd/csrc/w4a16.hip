@@ -765,8 +765,8 @@ __global__ __launch_bounds__(512) void w4a16_gemv_kernel(const W4Params p) {
   const int k0 = wave * 128 * IT;
 
   // Load order matters: the vector-memory counter retires loads in order, so the
-  // two activation pieces each thread stages are requested first, then this wave's
-  // weights (8 x 16 bytes per lane), then their scales and zero points. The staging
+  // activation pieces each thread stages are requested first, then the scales and
+  // zero points, then this wave's weights (IT x 16 bytes per lane). The staging
   // below waits for the activations only, and iteration i of the dot products for
   // weight load i only, so the arithmetic overlaps the weight stream.
   // blockDim = 64 * K / (128 IT), so every thread stages exactly MR * IT / 4 pieces of
@@ -782,16 +782,11 @@ __global__ __launch_bounds__(512) void w4a16_gemv_kernel(const W4Params p) {
     const u32x4 z = {0u, 0u, 0u, 0u};
     xin[e2] = r < p.m ? load16((const T*)p.x + (int64_t)r * p.x_stride + 8 * c8) : z;
   }
-  // this wave's weights, non-temporal; one descriptor over the workgroup's rows
-  // (rows past N read as zero)
+  // scales and zero points of this lane's pieces, then this wave's weights
+  // (one descriptor over the workgroup's rows, rows past N read as
+  // zero). The small loads go first: iteration i then waits for weight load i
+  // only, and the dot products run while the later weights stream in.
   const bool rok = row < p.n;
-  const int live_rows = min(16, p.n - n0);
-  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(p.qw + (int64_t)n0 * (K / 8), (uint32_t)live_rows * (uint32_t)(K / 2));
-  const int vrow = (lane >> 2) * (K / 2) + (k0 + 32 * pq) / 2;
-  u32x4 wv[IT];
-#pragma unroll
-  for (int i = 0; i < IT; ++i)
-    wv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, vrow, 64 * i, 0));
   const int esize = p.sdt == SS_DTYPE_F32 ? 4 : 2;
   const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.sc, (uint32_t)((int64_t)p.n * p.groups * esize));
   const __amdgpu_buffer_rsrc_t rzp = buffer_rsrc(p.qz, (uint32_t)((int64_t)p.n * p.groups * 4));
@@ -803,6 +798,13 @@ __global__ __launch_bounds__(512) void w4a16_gemv_kernel(const W4Params p) {
     sb[i] = scale_bits(rsc, gi, esize);
     zi[i] = __builtin_amdgcn_raw_buffer_load_b32(rzp, (int)(gi * 4), 0, 0);
   }
+  const int live_rows = min(16, p.n - n0);
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(p.qw + (int64_t)n0 * (K / 8), (uint32_t)live_rows * (uint32_t)(K / 2));
+  const int vrow = (lane >> 2) * (K / 2) + (k0 + 32 * pq) / 2;
+  u32x4 wv[IT];
+#pragma unroll
+  for (int i = 0; i < IT; ++i)
+    wv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, vrow, 64 * i, 0));
 
   // activations -> LDS (permuted to the nibble order), then per-32-key sums
 #pragma unroll
