@@ -84,7 +84,10 @@ int ss_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_ca
  * cache element (blk, off, h, d) = cache + blk*c_strides[0] + off*c_strides[1] + h*c_strides[2] + d
  * block_tables(b, i) = block_tables[b * bt_stride + i]
  * dtype: SS_DTYPE_BF16 or SS_DTYPE_F16 (q, cache and out share it).
- * workspace: device scratch of at least ss_paged_attention_workspace_size() bytes.
+ * workspace: device scratch of at least ss_paged_attention_workspace_size() bytes: the
+ * split-K decode partials (sized by occupancy) and, when max_query_len * n_q / n_kv
+ * exceeds 16 (prefill rows), the prefill work list (4 bytes per sequence and
+ * 128-row query tile), so the size depends on batch and max_query_len then.
  */
 int ss_paged_attention_workspace_size(int64_t batch, int n_q, int n_kv, int head_dim,
                                       int max_query_len, int dtype, int64_t* bytes);

@@ -7,7 +7,9 @@ namespace ss {
 int64_t decode_workspace_bytes(int dtype, int head_dim, int n_q, int n_kv, int max_query_len);
 int launch_decode(const AttnParams& p, int dtype, int head_dim, int max_query_len, char* ws,
                   int64_t ws_bytes, hipStream_t stream);
-int launch_prefill(const AttnParams& p, int dtype, int head_dim, int max_query_len, hipStream_t stream);
+int64_t prefill_work_bytes(int64_t batch, int n_rep, int max_query_len);
+int launch_prefill(const AttnParams& p, int dtype, int head_dim, int max_query_len, int* work,
+                   int64_t work_bytes, hipStream_t stream);
 }  // namespace ss
 
 namespace {
@@ -77,17 +79,33 @@ void fill_common(AttnParams& p, const void* q, void* out, const void* k_cache, c
   p.scale_log2 = scale * ss::kLog2e;
 }
 
+// Workspace layout: [decode split-K partials, 256-byte aligned][prefill work list].
+int64_t decode_part_bytes(int dtype, int head_dim, int n_q, int n_kv, int max_query_len) {
+  return (ss::decode_workspace_bytes(dtype, head_dim, n_q, n_kv, max_query_len) + 255) & ~(int64_t)255;
+}
+
 int run(AttnParams& p, int dtype, int head_dim, int max_query_len, void* workspace, int64_t ws_bytes,
         hipStream_t stream, bool decode_rows, bool prefill_rows) {
   p.rmax = ss::decode_rows_for(max_query_len, p.n_rep);
+  const int64_t dec_bytes = decode_part_bytes(dtype, head_dim, p.n_q, p.n_kv, max_query_len);
   auto decode = [&](hipStream_t s) {
     return ss::launch_decode(p, dtype, head_dim, max_query_len, (char*)workspace, ws_bytes, s);
   };
-  auto prefill = [&](hipStream_t s) { return ss::launch_prefill(p, dtype, head_dim, max_query_len, s); };
-  // A packed step has both kinds of rows: the decode part is bound by HBM and the
-  // prefill part by the matrix cores, and they write disjoint output rows, so the
-  // prefill runs on a side stream next to the decode.
-  if (decode_rows && prefill_rows) return ss_host::run_concurrently(stream, prefill, decode);
+  auto prefill = [&](hipStream_t s) {
+    const bool has_list = workspace && ws_bytes > dec_bytes;
+    return ss::launch_prefill(p, dtype, head_dim, max_query_len, has_list ? (int*)((char*)workspace + dec_bytes) : nullptr,
+                              has_list ? ws_bytes - dec_bytes : 0, s);
+  };
+  // A packed step has both kinds of rows. They run one after the other, the prefill
+  // first: each kernel fills every CU with one workgroup (registers, LDS), and the
+  // split-K decode finishes only when its last workgroup does, so sharing the GPU
+  // between them (a side stream) made whichever started second trickle in behind
+  // the first. The persistent prefill takes all CUs for its balanced share, then the
+  // decode gets all CUs at once.
+  if (decode_rows && prefill_rows) {
+    int st = prefill(stream);
+    return st != SS_OK ? st : decode(stream);
+  }
   if (decode_rows) return decode(stream);
   if (prefill_rows) return prefill(stream);
   return SS_OK;
@@ -97,14 +115,18 @@ int run(AttnParams& p, int dtype, int head_dim, int max_query_len, void* workspa
 
 extern "C" int ss_paged_attention_workspace_size(int64_t batch, int n_q, int n_kv, int head_dim,
                                                  int max_query_len, int dtype, int64_t* bytes) {
-  (void)batch;
   int st = check_common("paged attention workspace", n_q, n_kv, head_dim, 16, dtype, 0, 0);
   if (st != SS_OK) return st;
   if (!bytes) {
     ss_host::set_error("paged attention workspace: null output pointer");
     return SS_ERR_INVALID;
   }
-  *bytes = ss::decode_workspace_bytes(dtype, head_dim, n_q, n_kv, max_query_len < 1 ? 1 : max_query_len);
+  if (batch < 0) {
+    ss_host::set_error("paged attention workspace: negative batch");
+    return SS_ERR_INVALID;
+  }
+  const int mq = max_query_len < 1 ? 1 : max_query_len;
+  *bytes = decode_part_bytes(dtype, head_dim, n_q, n_kv, mq) + ss::prefill_work_bytes(batch, n_q / n_kv, mq);
   return SS_OK;
 }
 

@@ -21,6 +21,7 @@
 
 
 namespace ss {
+int64_t prefill_work_bytes(int64_t batch, int n_rep, int max_query_len);
 namespace {
 
 __device__ __attribute__((aligned(16))) uint32_t g_zero_row_p[128];
@@ -352,7 +353,8 @@ extern __shared__ __attribute__((aligned(1024))) char s_tile_stages[];
 // dynamic shared memory: a static size would make the compiler size registers
 // for the occupancy that size alone allows.
 template <typename T, int D>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_tile_kernel(const AttnParams p) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_tile_kernel(
+    const AttnParams p, const int* __restrict__ work) {
   typedef TileCfg<T, D> C;
   constexpr int NT = 1;              // 16-row MFMA tiles per wave
   constexpr int ROWS = 128;
@@ -363,7 +365,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   char* const vring = s_tile_stages;                  // V tile j in slot j % 3
   char* const kring = s_tile_stages + 3 * C::PLANE;   // K tile j in slot j % 3
 
-  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // Persistent workgroups walk the work list (prefill_plan_kernel: (sequence,
+  // 128-row query tile) entries, costliest first; entry e is the n_kv items
+  // e * n_kv + h, one per KV head) in snake order: round r takes item r*G + j, or
+  // r*G + G-1-j in odd rounds, so a workgroup that drew a long item early draws a
+  // short one next.
+  const int total = __builtin_amdgcn_readfirstlane(work[0]) * p.n_kv;
+  const int G = gridDim.x, wg = blockIdx.x;
+  for (int round = 0; round * G < total; ++round) {
+    const int idx = round * G + ((round & 1) ? G - 1 - wg : wg);
+    if (idx >= total) continue;
+    const int entry = idx / p.n_kv;
+    const int bq = __builtin_amdgcn_readfirstlane(work[1 + entry]);
+    [&](const int b, const int qt, const int h) {
   int qlen;
   int64_t qoff;
   seq_queries(p, b, qlen, qoff);
@@ -714,20 +728,92 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
   }
+    }(bq >> 16, bq & 0xFFFF, idx - entry * p.n_kv);
+    // the next item's loads land in LDS slots that other waves may still read
+    __syncthreads();
+  }
+}
+
+// Work list of the tiled prefill: work[0] = entries, work[1 + i] = (b << 16) | qt for
+// every (sequence, 128-row query tile) of a prefill sequence, ordered by decreasing
+// cost (64-key tiles below the tile's causal end, plus one): a counting sort over
+// cost buckets in LDS. Entries of equal cost land in any order; an item's result
+// does not depend on the workgroup that computes it.
+constexpr int kPlanBuckets = 1024;
+__global__ __launch_bounds__(1024) void prefill_plan_kernel(const AttnParams p, int* __restrict__ work,
+                                                             int qtiles) {
+  __shared__ int s_hist[kPlanBuckets];
+  __shared__ int s_base[kPlanBuckets];
+  const int tid = threadIdx.x;  // blockDim.x == kPlanBuckets
+  s_hist[tid] = 0;
+  __syncthreads();
+  const int64_t n_entries = (int64_t)p.batch * qtiles;
+  // cost bucket of entry e = b * qtiles + qt, or -1 when it is not a prefill tile
+  auto bucket = [&](int64_t e) {
+    const int b = (int)(e / qtiles), qt = (int)(e - (int64_t)b * qtiles);
+    int qlen;
+    int64_t qoff;
+    seq_queries(p, b, qlen, qoff);
+    if (qlen <= 0 || is_decode_seq(p, qlen)) return -1;
+    const int R = qlen * p.n_rep, row0 = qt * 128;
+    if (row0 >= R) return -1;
+    const int ctx = p.ctx_lens[b] < 0 ? 0 : p.ctx_lens[b];
+    const int kvt = seq_kv_tokens(p, ctx);
+    const int last_row = min(R - 1, row0 + 127);
+    const int kv_end = min(kvt, ctx - qlen + last_row / p.n_rep + 1);
+    const int cost = (kv_end > 0 ? (kv_end + 63) / 64 : 0) + 1;
+    return min(cost, kPlanBuckets - 1);
+  };
+  for (int64_t e = tid; e < n_entries; e += blockDim.x) {
+    const int c = bucket(e);
+    if (c >= 0) atomicAdd(&s_hist[c], 1);
+  }
+  __syncthreads();
+  {  // exclusive scan from the costliest bucket down: thread t takes bucket 1023 - t
+    __shared__ int s_wsum[kPlanBuckets / 64];
+    const int lane = tid & 63, wave = tid >> 6;
+    const int c = kPlanBuckets - 1 - tid;
+    int v = s_hist[c];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(v, o);
+      v += lane >= o ? t : 0;
+    }
+    if (lane == 63) s_wsum[wave] = v;
+    __syncthreads();
+    for (int w = 0; w < wave; ++w) v += s_wsum[w];
+    s_base[c] = v - s_hist[c];
+    if (tid == kPlanBuckets - 1) work[0] = v;
+  }
+  __syncthreads();
+  for (int64_t e = tid; e < n_entries; e += blockDim.x) {
+    const int c = bucket(e);
+    if (c >= 0) {
+      const int b = (int)(e / qtiles), qt = (int)(e - (int64_t)b * qtiles);
+      work[1 + atomicAdd(&s_base[c], 1)] = (b << 16) | qt;
+    }
+  }
 }
 
 constexpr int kPrefillNT = 2;
 
 template <typename T, int D>
-int launch_prefill_typed(const AttnParams& p, int max_query_len, hipStream_t stream) {
+int launch_prefill_typed(const AttnParams& p, int max_query_len, int* work, int64_t work_bytes,
+                         hipStream_t stream) {
   if (D <= 128 && p.block_size >= 16) {
     constexpr int rows = 128;
     const int64_t qtiles = ((int64_t)max_query_len * p.n_rep + rows - 1) / rows;
     if (qtiles < 1 || p.batch < 1) return SS_OK;
-    if (qtiles > 0x7fffffff || p.batch > 65535 || p.n_kv > 65535) {
-      ss_host::set_error("paged attention prefill: grid too large (tiles %lld, batch %d)", (long long)qtiles,
-                         p.batch);
+    if (qtiles > 0xFFFF || p.batch > 0x7FFF || (int64_t)p.batch * qtiles * p.n_kv > 0x7fffffff) {
+      ss_host::set_error("paged attention prefill: too many query tiles (%lld per sequence, batch %d)",
+                         (long long)qtiles, p.batch);
       return SS_ERR_UNSUPPORTED;
+    }
+    const int64_t need = prefill_work_bytes(p.batch, p.n_rep, max_query_len);
+    if (!work || work_bytes < need) {
+      ss_host::set_error("paged attention prefill: workspace of %lld bytes for the work list, needs %lld",
+                         (long long)work_bytes, (long long)need);
+      return SS_ERR_WORKSPACE;
     }
     constexpr int DD = D <= 128 ? D : 128;
     const int lds = 6 * TileCfg<T, DD>::PLANE;
@@ -740,8 +826,15 @@ int launch_prefill_typed(const AttnParams& p, int max_query_len, hipStream_t str
       }
       attr_set = true;
     }
-    hipLaunchKernelGGL((prefill_tile_kernel<T, DD>), dim3((unsigned)qtiles, p.n_kv, p.batch), dim3(512), lds,
-                       stream, p);
+    hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPlanBuckets), 0, stream, p, work, (int)qtiles);
+    int st = ss_host::launch_status("paged attention prefill plan");
+    if (st != SS_OK) return st;
+    // one resident workgroup per CU (the LDS rings take 96 KB); never more than items
+    const int64_t items = (int64_t)p.batch * qtiles * p.n_kv;
+    const int64_t cus = ss_host::device_cu_count();
+    const int grid = (int)(items < cus ? items : cus);
+    hipLaunchKernelGGL((prefill_tile_kernel<T, DD>), dim3((unsigned)grid), dim3(512), lds, stream, p,
+                       (const int*)work);
     return ss_host::launch_status("paged attention prefill");
   }
   typedef PrefillCfg<T, D, kPrefillNT> C;
@@ -760,15 +853,22 @@ int launch_prefill_typed(const AttnParams& p, int max_query_len, hipStream_t str
 
 }  // namespace
 
-int launch_prefill(const AttnParams& p, int dtype, int head_dim, int max_query_len, hipStream_t stream) {
+int64_t prefill_work_bytes(int64_t batch, int n_rep, int max_query_len) {
+  const int64_t rows = (int64_t)(max_query_len < 1 ? 1 : max_query_len) * n_rep;
+  if (rows <= kDecodeRows) return 0;  // no prefill rows
+  return 4 * (1 + batch * ((rows + 127) / 128));
+}
+
+int launch_prefill(const AttnParams& p, int dtype, int head_dim, int max_query_len, int* work,
+                   int64_t work_bytes, hipStream_t stream) {
   if (dtype == SS_DTYPE_BF16) {
-    if (head_dim == 64) return launch_prefill_typed<bf16_t, 64>(p, max_query_len, stream);
-    if (head_dim == 128) return launch_prefill_typed<bf16_t, 128>(p, max_query_len, stream);
-    return launch_prefill_typed<bf16_t, 256>(p, max_query_len, stream);
+    if (head_dim == 64) return launch_prefill_typed<bf16_t, 64>(p, max_query_len, work, work_bytes, stream);
+    if (head_dim == 128) return launch_prefill_typed<bf16_t, 128>(p, max_query_len, work, work_bytes, stream);
+    return launch_prefill_typed<bf16_t, 256>(p, max_query_len, work, work_bytes, stream);
   }
-  if (head_dim == 64) return launch_prefill_typed<f16_t, 64>(p, max_query_len, stream);
-  if (head_dim == 128) return launch_prefill_typed<f16_t, 128>(p, max_query_len, stream);
-  return launch_prefill_typed<f16_t, 256>(p, max_query_len, stream);
+  if (head_dim == 64) return launch_prefill_typed<f16_t, 64>(p, max_query_len, work, work_bytes, stream);
+  if (head_dim == 128) return launch_prefill_typed<f16_t, 128>(p, max_query_len, work, work_bytes, stream);
+  return launch_prefill_typed<f16_t, 256>(p, max_query_len, work, work_bytes, stream);
 }
 
 }  // namespace ss

@@ -5,7 +5,6 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include <functional>
 
 #include "../../include/slipstream_hip.h"
 
@@ -103,9 +102,4 @@ namespace ss_host {
 void set_error(const char* fmt, ...);
 int launch_status(const char* what);
 int device_cu_count();
-// Enqueue side_work on a per-device side stream and main_work on `stream` so that
-// they may run at the same time; `stream` waits for both before anything enqueued
-// on it later, and side_work starts only after everything enqueued on it before.
-int run_concurrently(hipStream_t stream, const std::function<int(hipStream_t)>& side_work,
-                     const std::function<int(hipStream_t)>& main_work);
 }  // namespace ss_host

@@ -53,9 +53,12 @@ def _check_cache(kv_cache: torch.Tensor, layer_idx: int, block_size: int, head_d
 
 def _workspace(device: torch.device, batch: int, n_q: int, n_kv: int, head_dim: int,
                max_query_len: int, dtype_code: int) -> torch.Tensor:
-    """Split-K scratch, sized by the library (it depends on occupancy, not on batch)."""
-    rows = min(16, max(1, max_query_len) * (n_q // n_kv))
-    key = (device.index, n_q, n_kv, head_dim, rows, dtype_code)
+    """Scratch sized by the library: the decode split-K partials (by occupancy) and,
+    when some sequence has prefill rows, the prefill work list (by batch and query tiles)."""
+    mq = max(1, max_query_len)
+    rows = mq * (n_q // n_kv)
+    # decode-only launches need the same bytes for every batch; prefill ones scale with it
+    key = (device.index, n_q, n_kv, head_dim, min(16, rows), dtype_code) + ((batch, mq) if rows > 16 else ())
     nbytes = _WS_BYTES.get(key)
     if nbytes is None:
         out = _ffi.ctypes.c_int64(0)
@@ -63,6 +66,8 @@ def _workspace(device: torch.device, batch: int, n_q: int, n_kv: int, head_dim: 
             batch, n_q, n_kv, head_dim, max(1, max_query_len), dtype_code, _ffi.ctypes.byref(out)
         )
         _ffi.check(status, "paged attention workspace")
+        if len(_WS_BYTES) > 4096:  # many distinct prefill batch shapes: start over
+            _WS_BYTES.clear()
         nbytes = _WS_BYTES[key] = max(int(out.value), 16)
     return torch.empty(nbytes, dtype=torch.uint8, device=device)
 

@@ -128,3 +128,33 @@ def test_build_step_metadata_argument_errors_need_no_device():
     assert lib.ss_build_step_metadata(None, 0, 0, None, None, 2, 0, None, None, None, 0, None) == _ffi.SS_ERR_INVALID
     assert lib.ss_build_step_metadata(None, 0, 0, None, None, 2, 16, None, None, None, 0, None) == _ffi.SS_ERR_INVALID
     assert b"null pointer" in lib.ss_last_error()
+
+
+def test_attention_workspace_holds_the_prefill_work_list():
+    """Decode-only launches need an occupancy-sized workspace whatever the batch; with
+    prefill rows the workspace also holds the prefill work list (a count plus one int32
+    per sequence and 128-row query tile), and a workspace without room for it is
+    SS_ERR_WORKSPACE before any HIP call."""
+    from slipstream_amd import _ffi
+
+    lib = _ffi.lib()
+    d = ctypes.c_int64(0)
+
+    def size(batch, max_query_len):
+        assert lib.ss_paged_attention_workspace_size(batch, 32, 8, 128, max_query_len, _ffi.SS_DTYPE_BF16,
+                                                     ctypes.byref(d)) == _ffi.SS_OK
+        return d.value
+
+    assert size(1, 1) == size(256, 1) > 0
+    assert size(196, 512) - size(4, 512) == 4 * (196 - 4) * (512 * 4 // 128)
+    assert lib.ss_paged_attention_workspace_size(-1, 32, 8, 128, 512, _ffi.SS_DTYPE_BF16,
+                                                 ctypes.byref(d)) == _ffi.SS_ERR_INVALID
+    # a padded prefill launch (Tq = 512 rows per sequence) whose workspace only fits the decode part
+    fake = 1 << 20  # 16-byte aligned, never dereferenced on the host
+    q_str = _ffi.i64_array([512 * 32 * 128, 128, 32 * 128])
+    o_str = _ffi.i64_array([512 * 32 * 128, 32 * 128, 128])
+    c_str = _ffi.i64_array([16 * 8 * 128, 8 * 128, 128])
+    st = lib.ss_paged_attention(fake, fake, fake, fake, fake, fake, 4, 32, 8, 128, 512, 64, 16, 1024,
+                                q_str, o_str, c_str, 64, 1.0, _ffi.SS_DTYPE_BF16, fake, size(4, 1), None)
+    assert st == _ffi.SS_ERR_WORKSPACE, lib.ss_last_error()
+    assert b"work list" in lib.ss_last_error()
