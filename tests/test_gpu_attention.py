@@ -408,8 +408,9 @@ def test_varlen_full_mixed_step_subset_checked(device):
 
 
 def test_varlen_packed_step_graph_replays(device):
-    """The packed step forks its prefill onto a side stream and joins it back with events;
-    captured in a HIP graph (after an eager warm-up), every replay equals the eager step."""
+    """The packed step (plan kernel writing the prefill work list into the workspace, the
+    persistent prefill, then the decode and its merge) captured in a HIP graph after an
+    eager warm-up: every replay equals the eager step, with eager steps in between."""
     ctx, ql = workloads.mixed_step_lengths(seed=9, n_prefill=2, chunk=80, n_decode=20)
     b = workloads.build_batch(ctx, ql, n_q=32, n_kv=8, head_dim=128, block_size=16, dtype=torch.bfloat16,
                               device=device, seed=9)
