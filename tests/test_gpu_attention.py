@@ -371,6 +371,39 @@ def test_varlen_mixed_step_reduced(device):
     assert_attn_close(out, _oracle_varlen(b, kv), "varlen mixed")
 
 
+def test_varlen_many_prefill_items_and_empty_sequences(device):
+    """The prefill work list at more items than resident workgroups (each persistent
+    workgroup walks several snake rounds: 856 items for 256 workgroups): 24 prefill
+    sequences with ragged query lengths (1-10 query tiles), decodes, short multi-token
+    queries and zero-length sequences interleaved, GQA 4:1; every row
+    against the oracle, and a repeat call is bit-identical (the order in which workgroups
+    take items does not change any item's result)."""
+    rng = np.random.default_rng(11)
+    ql, ctx = [], []
+    for i in range(54):
+        kind = i % 9
+        if kind in (0, 4):
+            ql.append(0), ctx.append(int(rng.integers(1, 200)))  # empty sequence
+        elif kind in (1, 5, 7):
+            q = int(rng.integers(2, 300))
+            ql.append(q), ctx.append(q + int(rng.integers(0, 400)))  # prefill, with or without prior
+        elif kind == 2:
+            ql.append(int(rng.integers(5, 17))), ctx.append(int(rng.integers(20, 300)))
+        else:
+            ql.append(1), ctx.append(int(rng.integers(1, 500)))  # decode
+    b = workloads.build_batch(ctx, ql, n_q=32, n_kv=8, head_dim=128, block_size=16, dtype=torch.bfloat16,
+                              device="cpu", seed=11)
+    kv_host = b.kv_cache.float().numpy().astype(np.float64)
+    _to(b, device)
+    out = paged_attention_varlen(b.q, b.kv_cache, b.block_tables, b.cu_seqlens, b.context_lens, 0, b.scale,
+                                 16, b.max_query_len)
+    again = paged_attention_varlen(b.q, b.kv_cache, b.block_tables, b.cu_seqlens, b.context_lens, 0,
+                                   b.scale, 16, b.max_query_len)
+    assert sum(1 for q in ql if q * 4 > 16) == 24
+    assert torch.equal(out, again)
+    assert_attn_close(out, _oracle_varlen(b, kv_host), "many prefill items")
+
+
 def test_varlen_equals_padded_calls(device):
     """Packed step == the per-sequence padded calls concatenated."""
     ctx, ql = [300, 45, 700, 64], [1, 1, 64, 32]
