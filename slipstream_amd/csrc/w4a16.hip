@@ -737,16 +737,18 @@ __global__ __launch_bounds__(256) void w4a16_generic_kernel(const W4Params p) {
 
 // Batch-1 (decode) W4A16 GEMV, shaped for HBM bandwidth rather than MFMA tiles.
 // A workgroup owns 16 weight rows; each of its waves owns one contiguous slice of
-// K (128 IT keys). Four consecutive lanes share a row and read its 64 contiguous
-// bytes (128 keys, one 16-byte load each), so a wave's load moves 16 full 64-byte
-// row segments; every wave issues all its loads up front, so the whole matrix is
+// K (128 IT keys). Eight consecutive lanes share a row and read 128 contiguous
+// bytes of it (256 keys, one 16-byte load each), so a load instruction moves 8
+// whole 128-byte lines (rows 0-7 or 8-15 of the workgroup), non-temporal: with
+// 4 lanes per row (16 half lines per instruction) the same weights streamed 5-13 %
+// slower. Every wave issues all its loads up front, so the whole matrix is
 // requested at once. The activation rows
 // are staged in LDS once per workgroup, permuted to the nibble order, with the
 // sum of every 32 keys. Per 16-byte piece (32 keys of one row, one quantisation
 // group as g % 32 == 0) a lane computes G = sum x (MAGIC + q) with v_dot2 and
-// folds s * (G - (MAGIC + z) * X); the four lanes of a row add by DPP, the waves'
-// slices add in LDS in wave order (no atomics: the result does not depend on
-// timing).
+// folds s * (G - (MAGIC + z) * X) into the sum of its row (two rows per lane); the
+// eight lanes of a row add by DPP, the waves' slices add in LDS in wave order (no
+// atomics: the result does not depend on timing).
 //
 // LDS: x [MR][K] permuted | chunk sums [K/32][MR] floats | slice partials [waves][16][MR] floats
 // MR: activation rows held (the kernel is used with MR = 1). IT: 128-key iterations
@@ -761,14 +763,16 @@ __global__ __launch_bounds__(512) void w4a16_gemv_kernel(const W4Params p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
   const int n0 = blockIdx.x * 16;
-  const int row = n0 + (lane >> 2), pq = lane & 3;
+  // lane: row rl of each 8-row group, 32-key piece q8 of each 256 keys; load u
+  // covers row group u & 1 and keys k0 + 256 (u >> 1) + 32 q8 .. + 31
+  const int rl = lane >> 3, q8 = lane & 7;
   const int k0 = wave * 128 * IT;
 
   // Load order matters: the vector-memory counter retires loads in order, so the
   // activation pieces each thread stages are requested first, then the scales and
   // zero points, then this wave's weights (IT x 16 bytes per lane). The staging
-  // below waits for the activations only, and iteration i of the dot products for
-  // weight load i only, so the arithmetic overlaps the weight stream.
+  // below waits for the activations only, and iteration u of the dot products for
+  // weight load u only, so the arithmetic overlaps the weight stream.
   // blockDim = 64 * K / (128 IT), so every thread stages exactly MR * IT / 4 pieces of
   // 8 keys.
   T* s_x = (T*)s_dyn;
@@ -782,29 +786,27 @@ __global__ __launch_bounds__(512) void w4a16_gemv_kernel(const W4Params p) {
     const u32x4 z = {0u, 0u, 0u, 0u};
     xin[e2] = r < p.m ? load16((const T*)p.x + (int64_t)r * p.x_stride + 8 * c8) : z;
   }
-  // scales and zero points of this lane's pieces, then this wave's weights
-  // (one descriptor over the workgroup's rows, rows past N read as
-  // zero). The small loads go first: iteration i then waits for weight load i
-  // only, and the dot products run while the later weights stream in.
-  const bool rok = row < p.n;
   const int esize = p.sdt == SS_DTYPE_F32 ? 4 : 2;
   const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.sc, (uint32_t)((int64_t)p.n * p.groups * esize));
   const __amdgpu_buffer_rsrc_t rzp = buffer_rsrc(p.qz, (uint32_t)((int64_t)p.n * p.groups * 4));
   uint32_t sb[IT];
   int zi[IT];
 #pragma unroll
-  for (int i = 0; i < IT; ++i) {
-    const int64_t gi = (int64_t)(rok ? row : 0) * p.groups + (k0 + 128 * i + 32 * pq) / p.g;
-    sb[i] = scale_bits(rsc, gi, esize);
-    zi[i] = __builtin_amdgcn_raw_buffer_load_b32(rzp, (int)(gi * 4), 0, 0);
+  for (int u = 0; u < IT; ++u) {
+    const int row = n0 + 8 * (u & 1) + rl;
+    const int64_t gi = (int64_t)(row < p.n ? row : 0) * p.groups + (k0 + 256 * (u >> 1) + 32 * q8) / p.g;
+    sb[u] = scale_bits(rsc, gi, esize);
+    zi[u] = __builtin_amdgcn_raw_buffer_load_b32(rzp, (int)(gi * 4), 0, 0);
   }
+  // one descriptor over the workgroup's rows (rows past N read as zero)
   const int live_rows = min(16, p.n - n0);
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(p.qw + (int64_t)n0 * (K / 8), (uint32_t)live_rows * (uint32_t)(K / 2));
-  const int vrow = (lane >> 2) * (K / 2) + (k0 + 32 * pq) / 2;
+  const int vrow = rl * (K / 2) + k0 / 2 + 16 * q8;
   u32x4 wv[IT];
 #pragma unroll
-  for (int i = 0; i < IT; ++i)
-    wv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, vrow, 64 * i, 0));
+  for (int u = 0; u < IT; ++u)
+    wv[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          rw, vrow, (u & 1) * 4 * K + 128 * (u >> 1), kNonTemporal));
 
   // activations -> LDS (permuted to the nibble order), then per-32-key sums
 #pragma unroll
@@ -827,19 +829,21 @@ __global__ __launch_bounds__(512) void w4a16_gemv_kernel(const W4Params p) {
   }
   __syncthreads();
 
-  // 3. dot products, one 32-key piece per iteration, folded per quantisation group
+  // dot products, one 32-key piece per iteration, folded per quantisation group
   const uint32_t magic = in_vgpr(E::kMagicPair);
-  float acc[MR];
+  float acc[2][MR];
 #pragma unroll
-  for (int r = 0; r < MR; ++r) acc[r] = 0.f;
+  for (int g2 = 0; g2 < 2; ++g2)
 #pragma unroll
-  for (int i = 0; i < IT; ++i) {
-    const int c = (k0 + 128 * i) / 32 + pq;
+    for (int r = 0; r < MR; ++r) acc[g2][r] = 0.f;
+#pragma unroll
+  for (int u = 0; u < IT; ++u) {
+    const int c = (k0 + 256 * (u >> 1)) / 32 + q8;
     u32x4 dq[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dq[j] = nibbles_to_operand(wv[i][j], magic);
-    const float zf = E::kMagic + (float)zi[i];
-    const float sci = decode_scale(sb[i], p.sdt);
+    for (int j = 0; j < 4; ++j) dq[j] = nibbles_to_operand(wv[u][j], magic);
+    const float zf = E::kMagic + (float)zi[u];
+    const float sci = decode_scale(sb[u], p.sdt);
 #pragma unroll
     for (int r = 0; r < MR; ++r) {
       float gsum = 0.f;
@@ -849,22 +853,25 @@ __global__ __launch_bounds__(512) void w4a16_gemv_kernel(const W4Params p) {
 #pragma unroll
         for (int h = 0; h < 4; ++h) gsum = dot2_acc<T>(dq[j][h], xv[h], gsum);
       }
-      acc[r] += sci * (gsum - zf * s_xs[c * MR + r]);
+      acc[u & 1][r] += sci * (gsum - zf * s_xs[c * MR + r]);
       // finish this iteration's dot products here: left to itself the compiler
       // unpacks every iteration's weights as they land and defers all dot products
-      // to the end, holding 8 x 16 unpacked registers (two workgroups per CU fewer)
-      asm volatile("" : "+v"(acc[r]));
+      // to the end, holding IT x 16 unpacked registers
+      asm volatile("" : "+v"(acc[u & 1][r]));
     }
   }
 
-  // 4. the four lanes of a row, then the waves' slices in order
+  // the eight lanes of a row, then the waves' slices in order
 #pragma unroll
-  for (int r = 0; r < MR; ++r) {
-    float v = acc[r];
-    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
-    if (pq == 0) s_part[(wave * 16 + (lane >> 2)) * MR + r] = v;
-  }
+  for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+      float v = acc[g2][r];
+      v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+      v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+      v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
+      if (q8 == 0) s_part[(wave * 16 + 8 * g2 + rl) * MR + r] = v;
+    }
   __syncthreads();
   if (threadIdx.x < 16 * MR) {
     const int rr = threadIdx.x / MR, r = threadIdx.x - rr * MR;
