@@ -121,6 +121,37 @@ int ss_paged_attention_varlen(const void* q, void* out, const void* k_cache, con
                               int64_t workspace_bytes, void* stream);
 
 /*
+ * Decode (one query token per sequence) for a batch whose block tables all begin
+ * with the same prefix_blocks physical blocks, the tables a prefix-cache hit
+ * produces (RadixPrefixCache.match / attach: slipstream/memory/prefix_cache.py:37-56,
+ * block_manager.py:91-98). Same result as paged_attention_decode
+ * (slipstream/kernels/paged_attention.py:21-40, ss_paged_attention with tq = 1) up to
+ * rounding, but the shared prefix is read once for the whole batch: its chunks are
+ * attended by every sequence's query rows together, the private suffixes by the
+ * decode, and the parts merged by log-sum-exp weights.
+ * Caller's promise: block_tables(b, i) == block_tables(0, i) for i < prefix_blocks and
+ * seq_lens[b] >= prefix_blocks * block_size for every b (not checked on the device).
+ * Batches with batch * n_q / n_kv <= 16, n_q / n_kv > 16, head_dim 256 or blocks of
+ * fewer than 16 tokens run the plain decode path instead.
+ * q(b, h, d) = q + b*q_strides[0] + h*q_strides[1] + d; out likewise with o_strides.
+ * workspace: at least ss_paged_attention_shared_prefix_workspace_size() bytes (the
+ * decode partials, the prefix pass's work list, chunk metadata, the parts' log-sum-exp
+ * and the prefix parts: S * batch * n_q * head_dim elements, S ~ CU count / (query
+ * tiles * n_kv)).
+ */
+int ss_paged_attention_shared_prefix_workspace_size(int64_t batch, int n_q, int n_kv, int head_dim,
+                                                    int block_size, int prefix_blocks, int dtype,
+                                                    int64_t* bytes);
+
+int ss_paged_attention_shared_prefix(const void* q, void* out, const void* k_cache, const void* v_cache,
+                                     const int32_t* block_tables, const int32_t* seq_lens, int64_t batch,
+                                     int n_q, int n_kv, int head_dim, int max_blocks, int block_size,
+                                     int64_t num_blocks, int prefix_blocks, const int64_t q_strides[2],
+                                     const int64_t o_strides[2], const int64_t c_strides[3],
+                                     int64_t bt_stride, float scale, int dtype, void* workspace,
+                                     int64_t workspace_bytes, void* stream);
+
+/*
  * W4A16 linear: out[m, :] = x[m, :] @ dequant(W)^T, no bias.
  * Replaces w4a16_gemm (slipstream/kernels/quant_gemm.py:23-42), whose body is
  * w4a16_gemm_ref (slipstream/kernels/quant_ref.py:119-133); weight format of

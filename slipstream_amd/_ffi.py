@@ -47,6 +47,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _c_i64p, _c_i64p, _c_i64p, _i64, ctypes.c_float, _i32, _vp, _i64, _vp,
         ],
     ),
+    "ss_paged_attention_shared_prefix_workspace_size": (_i32, [_i64, _i32, _i32, _i32, _i32, _i32, _i32, _c_i64p]),
+    "ss_paged_attention_shared_prefix": (
+        _i32,
+        [
+            _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i64, _i32,
+            _c_i64p, _c_i64p, _c_i64p, _i64, ctypes.c_float, _i32, _vp, _i64, _vp,
+        ],
+    ),
     "ss_paged_attention_varlen": (
         _i32,
         [

@@ -34,6 +34,10 @@ struct AttnParams {
   int hpw;               // KV heads per decode workgroup (one wave each)
   int n_hgroups;         // n_kv / hpw
   int rmax;              // query rows per (sequence, KV head) stored in a partial
+  // Shared-prefix cascade (zero / nullptr for plain attention):
+  float* lse;     // when set, log2-domain log-sum-exp of each query row: [tokens, n_q]
+  int noncausal;  // every query row sees all of its sequence's keys
+  int q_period;   // when > 0, query token t is read from row t % q_period
 };
 
 // Decode tile: one wave covers up to 16 query rows (query token j, head i in
@@ -51,6 +55,12 @@ __device__ __forceinline__ void seq_queries(const AttnParams& p, int b, int& qle
     qlen = p.tq;
     qoff = 0;
   }
+}
+
+// Index of a query row's log-sum-exp: packed token (or b * tq + t) times n_q, plus head.
+__device__ __forceinline__ int64_t lse_index(const AttnParams& p, int b, int64_t qoff, int j, int hq) {
+  const int64_t tok = p.cu ? qoff + j : (int64_t)b * p.tq + j;
+  return tok * p.n_q + hq;
 }
 
 // KV tokens reachable through the table (Triton: n_blocks = min(cdiv(len, bs), max_blocks)).

@@ -1,6 +1,8 @@
 // C-ABI entry points of paged attention: argument checks, then the split-K
 // decode kernel for sequences whose query rows fit one 16-row MFMA tile, and
 // the prefill kernel for the rest.
+#include <algorithm>
+
 #include "attention_common.h"
 
 namespace ss {
@@ -220,4 +222,275 @@ extern "C" int ss_paged_attention_varlen(const void* q, void* out, const void* k
   const bool prefill = (int64_t)max_query_len * p.n_rep > ss::kDecodeRows;
   return run(p, dtype, head_dim, max_query_len, workspace, workspace_bytes, (hipStream_t)stream, true,
              prefill);
+}
+
+// ---- shared-prefix cascade -------------------------------------------------
+//
+// A decode batch whose block tables all begin with the same prefix_blocks blocks
+// (prefix-cache hits share full blocks) attends that prefix once for every
+// sequence's query rows instead of once per sequence:
+//   1. the prefix is cut into S chunks of cb blocks; chunk s is a pseudo-sequence
+//      whose queries are the whole batch's (read in place, token t from row
+//      t % batch) and whose keys are the chunk, without a causal mask. The tiled
+//      prefill computes every (chunk, batch row) partial and its log-sum-exp;
+//   2. the decode attends each sequence's private suffix through its table
+//      shifted by prefix_blocks, writing the suffix part and its log-sum-exp into
+//      out;
+//   3. a combine weighs the S + 1 normalised parts by 2^(lse - max).
+// Softmax over a union of disjoint key sets is the lse-weighted mix of the parts'
+// softmaxes, so the result is the plain decode's up to rounding.
+
+namespace {
+
+using ss::bf16_t;
+using ss::f16_t;
+using ss::f16x2;
+using ss::u32x4;
+using ss::Elem;
+using ss::fast_exp2;
+using ss::load16;
+using ss::store16;
+
+struct PrefixPlan {
+  bool cascade = false;
+  int cb = 0, S = 0;
+  int64_t dec = 0, work = 0, meta = 0, lse = 0, part = 0;
+  int64_t total() const { return dec + work + meta + lse + part; }
+};
+
+int64_t round256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+PrefixPlan prefix_plan(int64_t batch, int n_q, int n_kv, int head_dim, int block_size, int prefix_blocks,
+                       int dtype) {
+  PrefixPlan pl;
+  const int n_rep = n_q / n_kv;
+  pl.dec = decode_part_bytes(dtype, head_dim, n_q, n_kv, 1);
+  // the prefill's tiled kernel (head_dim <= 128, blocks of 16+ tokens) carries the
+  // prefix pass and the decode kernel the suffixes (n_rep <= 16); other shapes, and
+  // batches whose rows fit one decode tile, take the plain path of one query token
+  pl.cascade = prefix_blocks > 0 && head_dim <= 128 && block_size >= 16 && n_rep <= ss::kDecodeRows &&
+               batch * n_rep > ss::kDecodeRows;
+  if (!pl.cascade) {
+    pl.work = ss::prefill_work_bytes(batch, n_rep, 1);
+    return pl;
+  }
+  // about one prefill item per CU: items = S * row tiles * n_kv; chunks hold
+  // whole 64-key tiles
+  const int64_t per_chunk = ((batch * n_rep + 127) / 128) * n_kv;
+  const int64_t cus = ss_host::device_cu_count();
+  int64_t target = (cus + per_chunk - 1) / per_chunk;
+  if (target < 1) target = 1;
+  const int tile_blocks = 64 / block_size > 1 ? 64 / block_size : 1;
+  int64_t cb = (prefix_blocks + target - 1) / target;
+  cb = (cb + tile_blocks - 1) / tile_blocks * tile_blocks;
+  pl.cb = (int)cb;
+  pl.S = (int)((prefix_blocks + cb - 1) / cb);
+  const int64_t elem = 2;  // bf16 / fp16
+  pl.work = round256(ss::prefill_work_bytes(pl.S, n_rep, (int)batch));
+  pl.meta = round256(4 * ((int64_t)pl.S + 1 + pl.S + batch + (int64_t)pl.S * pl.cb));
+  pl.lse = round256(4 * ((int64_t)pl.S + 1) * batch * n_q);
+  pl.part = round256((int64_t)pl.S * batch * n_q * head_dim * elem);
+  return pl;
+}
+
+// meta = [cu: S + 1][chunk lengths: S][suffix lengths: batch][chunk tables: S * cb]
+__global__ __launch_bounds__(256) void prefix_setup_kernel(const int32_t* __restrict__ bt,
+                                                           const int32_t* __restrict__ seq_lens, int batch, int S,
+                                                           int cb, int prefix_blocks, int block_size,
+                                                           int32_t* __restrict__ meta) {
+  int32_t* cu = meta;
+  int32_t* pctx = cu + S + 1;
+  int32_t* sctx = pctx + S;
+  int32_t* ptab = sctx + batch;
+  const int n = max(max(S + 1, batch), S * cb);
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    if (i <= S) cu[i] = i * batch;
+    if (i < S) pctx[i] = min(cb, prefix_blocks - i * cb) * block_size;
+    if (i < batch) sctx[i] = max(seq_lens[i] - prefix_blocks * block_size, 0);
+    // past the prefix the chunk table repeats its last block: a valid block that no
+    // key position below a chunk's length reaches
+    if (i < S * cb) ptab[i] = bt[min(i, prefix_blocks - 1)];
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float half_to_f32(uint32_t w, int hi);
+template <>
+__device__ __forceinline__ float half_to_f32<bf16_t>(uint32_t w, int hi) {
+  return __builtin_bit_cast(float, hi ? (w & 0xFFFF0000u) : (w << 16));
+}
+template <>
+__device__ __forceinline__ float half_to_f32<f16_t>(uint32_t w, int hi) {
+  return (float)__builtin_bit_cast(f16x2, w)[hi];
+}
+
+// One thread per (sequence, query head, 8 consecutive d): out = sum_i 2^(lse_i - M) o_i
+// / sum_i 2^(lse_i - M) over the suffix part (already in out) and the S prefix parts.
+template <typename T>
+__global__ __launch_bounds__(256) void prefix_combine_kernel(const T* __restrict__ part,
+                                                             const float* __restrict__ part_lse,
+                                                             const float* __restrict__ sfx_lse, T* out,
+                                                             int64_t o_sb, int64_t o_sh, int batch, int n_q,
+                                                             int head_dim, int S) {
+  const int dv = head_dim / 8;
+  const int64_t rows = (int64_t)batch * n_q;
+  const int64_t total = rows * dv;
+  for (int64_t u = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; u < total;
+       u += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(u % dv);
+    const int64_t bh = u / dv;
+    const int b = (int)(bh / n_q), hq = (int)(bh - (int64_t)b * n_q);
+    T* o = out + b * o_sb + hq * o_sh + 8 * c;
+    const float ls = sfx_lse[bh];
+    float mx = ls;
+    for (int s = 0; s < S; ++s) mx = fmaxf(mx, part_lse[s * rows + bh]);
+    // every chunk holds at least one key, so mx is finite; a -inf part weighs 0
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float wsum = 0.f;
+    auto add = [&](const u32x4 v, float lse) {
+      const float w = fast_exp2(lse - mx);
+      wsum += w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] += w * half_to_f32<T>(v[e], 0);
+        acc[2 * e + 1] += w * half_to_f32<T>(v[e], 1);
+      }
+    };
+    add(load16(o), ls);
+    for (int s = 0; s < S; ++s) add(load16(part + (s * rows + bh) * head_dim + 8 * c), part_lse[s * rows + bh]);
+    const float inv = 1.f / wsum;
+    store16(o, u32x4{Elem<T>::pack2(acc[0] * inv, acc[1] * inv), Elem<T>::pack2(acc[2] * inv, acc[3] * inv),
+                     Elem<T>::pack2(acc[4] * inv, acc[5] * inv), Elem<T>::pack2(acc[6] * inv, acc[7] * inv)});
+  }
+}
+
+}  // namespace
+
+extern "C" int ss_paged_attention_shared_prefix_workspace_size(int64_t batch, int n_q, int n_kv, int head_dim,
+                                                               int block_size, int prefix_blocks, int dtype,
+                                                               int64_t* bytes) {
+  const char* who = "shared-prefix attention workspace";
+  int st = check_common(who, n_q, n_kv, head_dim, block_size, dtype, 0, 0);
+  if (st != SS_OK) return st;
+  if (!bytes) {
+    ss_host::set_error("%s: null output pointer", who);
+    return SS_ERR_INVALID;
+  }
+  if (batch < 0 || prefix_blocks < 0) {
+    ss_host::set_error("%s: negative batch or prefix_blocks", who);
+    return SS_ERR_INVALID;
+  }
+  *bytes = prefix_plan(batch, n_q, n_kv, head_dim, block_size, prefix_blocks, dtype).total();
+  return SS_OK;
+}
+
+extern "C" int ss_paged_attention_shared_prefix(const void* q, void* out, const void* k_cache, const void* v_cache,
+                                                const int32_t* block_tables, const int32_t* seq_lens, int64_t batch,
+                                                int n_q, int n_kv, int head_dim, int max_blocks, int block_size,
+                                                int64_t num_blocks, int prefix_blocks, const int64_t q_strides[2],
+                                                const int64_t o_strides[2], const int64_t c_strides[3],
+                                                int64_t bt_stride, float scale, int dtype, void* workspace,
+                                                int64_t workspace_bytes, void* stream) {
+  const char* who = "shared-prefix attention";
+  int st = check_common(who, n_q, n_kv, head_dim, block_size, dtype, max_blocks, num_blocks);
+  if (st != SS_OK) return st;
+  if (batch < 0 || prefix_blocks < 0 || prefix_blocks > max_blocks) {
+    ss_host::set_error("%s: need batch >= 0 and 0 <= prefix_blocks <= max_blocks (got %lld, %d, %d)", who,
+                       (long long)batch, prefix_blocks, max_blocks);
+    return SS_ERR_INVALID;
+  }
+  if (batch == 0) return SS_OK;
+  if (batch > 0x7FFFFF) {
+    ss_host::set_error("%s: batch %lld too large", who, (long long)batch);
+    return SS_ERR_UNSUPPORTED;
+  }
+  if ((st = check_strides(who, q_strides, 2)) != SS_OK) return st;
+  if ((st = check_strides(who, o_strides, 2)) != SS_OK) return st;
+  if ((st = check_strides(who, c_strides, 3)) != SS_OK) return st;
+  if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache)) {
+    ss_host::set_error("%s: q, out and cache planes must be 16-byte aligned", who);
+    return SS_ERR_UNSUPPORTED;
+  }
+  if (!block_tables || !seq_lens) {
+    ss_host::set_error("%s: null block_tables or seq_lens", who);
+    return SS_ERR_INVALID;
+  }
+  const PrefixPlan pl = prefix_plan(batch, n_q, n_kv, head_dim, block_size, prefix_blocks, dtype);
+  if (!workspace || workspace_bytes < pl.total()) {
+    ss_host::set_error("%s: workspace of %lld bytes, needs %lld", who, (long long)workspace_bytes,
+                       (long long)pl.total());
+    return SS_ERR_WORKSPACE;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  AttnParams p = {};
+  fill_common(p, q, out, k_cache, v_cache, block_tables, seq_lens, batch, n_q, n_kv, max_blocks, block_size,
+              num_blocks, c_strides, bt_stride, scale);
+  p.cu = nullptr;
+  p.tq = 1;
+  p.q_sb = q_strides[0];
+  p.q_sh = q_strides[1];
+  p.q_st = 0;
+  p.o_sb = o_strides[0];
+  p.o_sh = o_strides[1];
+  p.o_st = 0;
+  if (!pl.cascade) {
+    const bool dec = p.n_rep <= ss::kDecodeRows;
+    return run(p, dtype, head_dim, 1, ws, pl.dec + pl.work, s, dec, !dec);
+  }
+
+  int32_t* meta = (int32_t*)(ws + pl.dec + pl.work);
+  float* lse = (float*)(ws + pl.dec + pl.work + pl.meta);
+  void* part = ws + pl.dec + pl.work + pl.meta + pl.lse;
+  const int64_t rows = batch * n_q;
+  {
+    const int n = std::max<int64_t>(std::max<int64_t>(pl.S + 1, batch), (int64_t)pl.S * pl.cb);
+    hipLaunchKernelGGL(prefix_setup_kernel, dim3((n + 255) / 256), dim3(256), 0, s, block_tables, seq_lens,
+                       (int)batch, pl.S, pl.cb, prefix_blocks, block_size, meta);
+    if ((st = ss_host::launch_status("shared-prefix setup")) != SS_OK) return st;
+  }
+  const int32_t* cu = meta;
+  const int32_t* pctx = cu + pl.S + 1;
+  const int32_t* sctx = pctx + pl.S;
+  const int32_t* ptab = sctx + batch;
+  {  // 1. prefix chunks as pseudo-sequences of the prefill, queries read in place
+    AttnParams pp = {};
+    fill_common(pp, q, part, k_cache, v_cache, ptab, pctx, pl.S, n_q, n_kv, pl.cb, block_size, num_blocks,
+                c_strides, pl.cb, scale);
+    pp.cu = cu;
+    pp.q_sb = 0;
+    pp.q_st = q_strides[0];
+    pp.q_sh = q_strides[1];
+    pp.o_sb = 0;
+    pp.o_st = (int64_t)n_q * head_dim;
+    pp.o_sh = head_dim;
+    pp.rmax = ss::decode_rows_for((int)batch, pp.n_rep);
+    pp.lse = lse;
+    pp.noncausal = 1;
+    pp.q_period = (int)batch;
+    st = ss::launch_prefill(pp, dtype, head_dim, (int)batch, (int*)(ws + pl.dec), pl.work, s);
+    if (st != SS_OK) return st;
+  }
+  {  // 2. private suffixes: the table from column prefix_blocks on
+    AttnParams ps = p;
+    ps.bt = block_tables + prefix_blocks;
+    ps.max_blocks = max_blocks - prefix_blocks;
+    ps.ctx_lens = sctx;
+    ps.lse = lse + (int64_t)pl.S * rows;
+    ps.rmax = ss::decode_rows_for(1, ps.n_rep);
+    st = ss::launch_decode(ps, dtype, head_dim, 1, ws, pl.dec, s);
+    if (st != SS_OK) return st;
+  }
+  // 3. combine
+  const int64_t threads = rows * (head_dim / 8);
+  const int grid = (int)std::min<int64_t>((threads + 255) / 256, 8192);
+  if (dtype == SS_DTYPE_BF16)
+    hipLaunchKernelGGL(prefix_combine_kernel<bf16_t>, dim3(grid), dim3(256), 0, s, (const bf16_t*)part, lse,
+                       lse + (int64_t)pl.S * rows, (bf16_t*)out, o_strides[0], o_strides[1], (int)batch, n_q,
+                       head_dim, pl.S);
+  else
+    hipLaunchKernelGGL(prefix_combine_kernel<f16_t>, dim3(grid), dim3(256), 0, s, (const f16_t*)part, lse,
+                       lse + (int64_t)pl.S * rows, (f16_t*)out, o_strides[0], o_strides[1], (int)batch, n_q,
+                       head_dim, pl.S);
+  return ss_host::launch_status("shared-prefix combine");
 }

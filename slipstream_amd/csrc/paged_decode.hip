@@ -363,6 +363,7 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
       if (complete) {
         if (row_ok) {
           const float inv = lt > 0.f ? 1.f / lt : 0.f;
+          if (p.lse && g == 0) p.lse[lse_index(p, b, qoff, j, hq)] = row_lse(st.m, lt);
           T* orow = (T*)p.out + (int64_t)b * p.o_sb + (qoff + j) * p.o_st + (int64_t)hq * p.o_sh;
 #pragma unroll
           for (int mt = 0; mt < Tile::MT; ++mt) {
@@ -641,6 +642,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const AttnParams p, i
       const int hq = rem / D, d = rem - hq * D;
       T* o = (T*)p.out + (int64_t)b * p.o_sb + (qoff + j) * p.o_st + (int64_t)hq * p.o_sh + d;
       *o = (T)0.f;
+      if (p.lse && d == 0) p.lse[lse_index(p, b, qoff, j, hq)] = -__builtin_inff();
     }
     return;
   }
@@ -703,6 +705,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const AttnParams p, i
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
     const int j = r / p.n_rep;
     const int hq = (hg * p.hpw + wave) * p.n_rep + (r - j * p.n_rep);
+    if (p.lse && c == 0) p.lse[lse_index(p, b, qoff, j, hq)] = row_lse(mmax, lsum);
     T* o = (T*)p.out + (int64_t)b * p.o_sb + (qoff + j) * p.o_st + (int64_t)hq * p.o_sh + 8 * c;
     store16(o, u32x4{Elem<T>::pack2(o0[0] * inv, o0[1] * inv), Elem<T>::pack2(o0[2] * inv, o0[3] * inv),
                      Elem<T>::pack2(o1[0] * inv, o1[1] * inv), Elem<T>::pack2(o1[2] * inv, o1[3] * inv)});

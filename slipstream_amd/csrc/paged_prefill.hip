@@ -397,7 +397,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int ctx = __builtin_amdgcn_readfirstlane(p.ctx_lens[b] < 0 ? 0 : p.ctx_lens[b]);
   const int kvt = seq_kv_tokens(p, ctx);
   const int last_row = min(R - 1, row0 + ROWS - 1);
-  const int kv_end = min(kvt, ctx - qlen + last_row / p.n_rep + 1);
+  const int kv_end = p.noncausal ? kvt : min(kvt, ctx - qlen + last_row / p.n_rep + 1);
   const int ntiles = kv_end > 0 ? (kv_end + C::KT - 1) / C::KT : 0;
   const ConstTable table = (ConstTable)(p.bt + (int64_t)b * p.bt_stride);
 
@@ -413,9 +413,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const bool ok = rr < R;
     const int j = ok ? rr / p.n_rep : 0;
     const int hq = h * p.n_rep + (ok ? rr - j * p.n_rep : 0);
-    const int l = ctx - qlen + j + 1;
+    const int l = p.noncausal ? kvt : ctx - qlen + j + 1;
     lim[nt] = ok ? (l < kvt ? l : kvt) : kvt;
-    const T* qrow = (const T*)p.q + (int64_t)b * p.q_sb + (qoff + j) * p.q_st + (int64_t)hq * p.q_sh;
+    const int64_t qtok = p.q_period > 0 ? (qoff + j) % p.q_period : qoff + j;
+    const T* qrow = (const T*)p.q + (int64_t)b * p.q_sb + qtok * p.q_st + (int64_t)hq * p.q_sh;
 #pragma unroll
     for (int s = 0; s < C::KS; ++s) {
       const u32x4 z = {0u, 0u, 0u, 0u};
@@ -428,7 +429,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   wait_vm<0>();
   // smallest causal limit over the wave's rows (rows past R do not count)
   const int wrow = min(row0 + wave * 16 * NT, R - 1);
-  const int wave_lim = min(kvt, ctx - qlen + wrow / p.n_rep + 1);
+  const int wave_lim = p.noncausal ? kvt : min(kvt, ctx - qlen + wrow / p.n_rep + 1);
 
   const int tok_bytes = (int)(p.c_so * (int64_t)sizeof(T));
   const int64_t blk_bytes = p.c_sb * (int64_t)sizeof(T);
@@ -716,6 +717,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const int j = rr / p.n_rep;
       const int hq = h * p.n_rep + (rr - j * p.n_rep);
       const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      if (p.lse && g == 0) p.lse[lse_index(p, b, qoff, j, hq)] = row_lse(mrow[nt], lt);
       T* orow = (T*)p.out + (int64_t)b * p.o_sb + (qoff + j) * p.o_st + (int64_t)hq * p.o_sh + (D / 4) * g;
 #pragma unroll
       for (int w = 0; w < C::DT / 2; ++w) {
@@ -760,7 +762,7 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const AttnParams p, 
     const int ctx = p.ctx_lens[b] < 0 ? 0 : p.ctx_lens[b];
     const int kvt = seq_kv_tokens(p, ctx);
     const int last_row = min(R - 1, row0 + 127);
-    const int kv_end = min(kvt, ctx - qlen + last_row / p.n_rep + 1);
+    const int kv_end = p.noncausal ? kvt : min(kvt, ctx - qlen + last_row / p.n_rep + 1);
     const int cost = (kv_end > 0 ? (kv_end + 63) / 64 : 0) + 1;
     return min(cost, kPlanBuckets - 1);
   };

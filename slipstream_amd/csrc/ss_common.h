@@ -89,6 +89,10 @@ __device__ __forceinline__ float sum_across_rows(float x) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+// log2-domain log-sum-exp of a softmax row from its running (max, sum); -inf for no key.
+__device__ __forceinline__ float row_lse(float m, float l) {
+  return l > 0.f ? m + __builtin_amdgcn_logf(l) : -__builtin_inff();
+}
 
 __device__ __forceinline__ u32x4 load16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);

@@ -5,6 +5,7 @@ from slipstream_amd.kernels.paged_attention import (
     paged_attention,
     paged_attention_decode,
     paged_attention_prefill,
+    paged_attention_shared_prefix,
     paged_attention_varlen,
 )
 from slipstream_amd.kernels.norm_act import fused_rmsnorm, fused_swiglu
@@ -21,6 +22,7 @@ __all__ = [
     "paged_attention",
     "paged_attention_decode",
     "paged_attention_prefill",
+    "paged_attention_shared_prefix",
     "paged_attention_varlen",
     "reshape_and_cache",
     "rope_and_cache",

@@ -161,6 +161,102 @@ def paged_attention_decode(
     return paged_attention(q, kv_cache, block_tables, seq_lens, layer_idx, scale, block_size)
 
 
+_PREFIX_WS: dict[tuple, int] = {}
+
+
+def paged_attention_shared_prefix(
+    q: torch.Tensor,
+    kv_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    layer_idx: int,
+    scale: float,
+    block_size: int,
+    prefix_blocks: int,
+) -> torch.Tensor:
+    """Decode of ``q`` ``[B, n_q, 1, D]`` for a batch whose block tables all begin with
+    the same ``prefix_blocks`` blocks (a prefix-cache hit: ``prefix_cache.py:37-56``
+    shares full blocks, ``block_manager.py:91-98`` attaches them). Returns what
+    ``paged_attention_decode`` (``kernels/paged_attention.py:21-40``) returns, up to
+    rounding, while reading the shared prefix once for the batch instead of once per
+    sequence. The caller promises ``block_tables[:, :prefix_blocks]`` equal to row 0 in
+    every row and ``seq_lens >= prefix_blocks * block_size``; neither is checked on the
+    device (``SLIPSTREAM_DEBUG`` checks both on the host)."""
+    if q.ndim != 4 or q.shape[2] != 1:
+        raise ValueError(f"q must be [B, n_q, 1, D], got {tuple(q.shape)}")
+    batch, n_q, _, head_dim = q.shape
+    _check_cache(kv_cache, layer_idx, block_size, head_dim)
+    n_kv = int(kv_cache.shape[4])
+    if n_kv == 0 or n_q % n_kv != 0:
+        raise ValueError(f"GQA requires n_q % n_kv == 0, got n_q={n_q} n_kv={n_kv}")
+    if block_tables.ndim != 2 or block_tables.shape[0] != batch:
+        raise ValueError(f"block_tables must be [B={batch}, max_blocks], got {tuple(block_tables.shape)}")
+    if seq_lens.numel() != batch:
+        raise ValueError(f"seq_lens has {seq_lens.numel()} entries for batch {batch}")
+    if not 0 <= prefix_blocks <= block_tables.shape[1]:
+        raise ValueError(f"prefix_blocks {prefix_blocks} outside [0, {block_tables.shape[1]}]")
+    if batch == 0 or n_q == 0:
+        return q.new_empty((batch, 1, n_q, head_dim))
+    require_device("paged_attention_shared_prefix", q, kv_cache, block_tables, seq_lens)
+    if q.dtype not in _SUPPORTED or kv_cache.dtype != q.dtype:
+        raise _ffi.KernelError(
+            f"unsupported dtypes q={q.dtype} kv_cache={kv_cache.dtype} (bf16/fp16, equal)"
+        )
+    q = unit_last_stride(q)
+    block_tables = _int32(block_tables)
+    seq_lens = _int32(seq_lens.reshape(-1))
+    if _debug() and prefix_blocks > 0:
+        if not bool((block_tables[:, :prefix_blocks] == block_tables[:1, :prefix_blocks]).all()):
+            raise ValueError("block_tables rows differ inside the shared prefix")
+        if int(seq_lens.min()) < prefix_blocks * block_size:
+            raise ValueError("a sequence is shorter than the shared prefix")
+    kc = kv_cache[layer_idx, 0]
+    vc = kv_cache[layer_idx, 1]
+    if kc.stride(3) != 1 or kc.data_ptr() % 16 or vc.data_ptr() % 16:
+        raise _ffi.KernelError("kv_cache planes must have unit head_dim stride and 16-byte alignment")
+    out = torch.empty((batch, 1, n_q, head_dim), device=q.device, dtype=q.dtype)
+    code = _ffi.dtype_code(q.dtype)
+    key = (q.device.index, batch, n_q, n_kv, head_dim, block_size, prefix_blocks, code)
+    nbytes = _PREFIX_WS.get(key)
+    if nbytes is None:
+        size = _ffi.ctypes.c_int64(0)
+        status = _ffi.lib().ss_paged_attention_shared_prefix_workspace_size(
+            batch, n_q, n_kv, head_dim, block_size, prefix_blocks, code, _ffi.ctypes.byref(size)
+        )
+        _ffi.check(status, "shared-prefix attention workspace")
+        if len(_PREFIX_WS) > 4096:
+            _PREFIX_WS.clear()
+        nbytes = _PREFIX_WS[key] = max(int(size.value), 16)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    status = _ffi.lib().ss_paged_attention_shared_prefix(
+        q.data_ptr(),
+        out.data_ptr(),
+        kc.data_ptr(),
+        vc.data_ptr(),
+        block_tables.data_ptr(),
+        seq_lens.data_ptr(),
+        batch,
+        n_q,
+        n_kv,
+        head_dim,
+        block_tables.shape[1],
+        block_size,
+        kv_cache.shape[2],
+        prefix_blocks,
+        _ffi.i64_array(_strides(q, (0, 1))),
+        _ffi.i64_array(_strides(out, (0, 2))),
+        _ffi.i64_array([kc.stride(0), kc.stride(1), kc.stride(2)]),
+        block_tables.stride(0),
+        float(scale),
+        code,
+        ws.data_ptr(),
+        ws.numel(),
+        _ffi.stream_ptr(q.device),
+    )
+    _ffi.check(status, "paged_attention_shared_prefix")
+    return out
+
+
 def paged_attention_prefill(
     q: torch.Tensor,
     kv_cache: torch.Tensor,

@@ -1,0 +1,119 @@
+"""GPU parity of the shared-prefix decode (prefix pass + suffix decode + log-sum-exp
+combine) against the numpy oracle of ``paged_attention_ref`` (``attention_ref.py:68-89``).
+
+The cascade reorders the softmax sum (prefix chunks and the suffix are normalised apart,
+then mixed by ``2^(lse - max)``), so it matches the oracle to the attention tolerance, not
+bit for bit. Batches whose query rows fit one decode tile, head_dim 256 and blocks under
+16 tokens take the plain decode inside the same entry point, covered here too.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_attention as ora
+from slipstream_amd import workloads
+from slipstream_amd.kernels import paged_attention_decode, paged_attention_shared_prefix
+from tests._helpers import assert_attn_close, f64, tables_array
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle(b: workloads.PagedBatch, rows=None) -> np.ndarray:
+    rows = list(range(b.batch)) if rows is None else rows
+    kv = f64(b.kv_cache)
+    tables = tables_array([b.tables_host[i] for i in rows], b.block_tables.shape[1])
+    q = f64(b.padded_q()[rows])
+    ctx = np.array([b.ctx_host[i] for i in rows])
+    return ora.paged_attention(q, kv, tables, ctx, 0, b.scale, b.block_size)
+
+
+def _run(b: workloads.PagedBatch, prefix_blocks: int) -> torch.Tensor:
+    return paged_attention_shared_prefix(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale,
+                                         b.block_size, prefix_blocks)
+
+
+def test_c4_shape_reduced_batch(device):
+    """C4 shape (28/4 heads, D 128, 2048-token prefix) at batch 32: 224 query rows per
+    KV head, so the prefix pass runs."""
+    b = workloads.prefix_share(device=device, seed=5, batch=32)
+    out = _run(b, b.shared_blocks)
+    assert out.shape == (32, 1, 28, 128) and out.dtype == torch.bfloat16
+    assert_attn_close(out, _oracle(b), "c4 reduced")
+
+
+def test_c4_full_config(device):
+    """The full C4 batch (128 sequences): every row within tolerance of the plain decode,
+    a subset of rows against the oracle."""
+    b = workloads.prefix_share(device=device, seed=0)
+    out = _run(b, b.shared_blocks)
+    plain = paged_attention_decode(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
+    torch.testing.assert_close(out.float(), plain.float(), atol=2e-3, rtol=1e-2)
+    rows = [0, 1, 63, 127]
+    assert_attn_close(out[rows], _oracle(b, rows), "c4 subset")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n_q,n_kv,head_dim,block_size,prefix_blocks,batch", [
+    (28, 4, 128, 16, 37, 24),   # prefix not a whole number of chunks
+    (32, 8, 128, 16, 64, 40),   # GQA 4
+    (8, 8, 64, 16, 20, 48),     # MHA, head_dim 64
+    (16, 1, 128, 32, 9, 8),     # MQA, 32-token blocks
+    (28, 4, 128, 16, 1, 20),    # one shared block
+])
+def test_shapes_and_empty_suffixes(device, dtype, n_q, n_kv, head_dim, block_size, prefix_blocks, batch):
+    """Suffix lengths include 0 (the sequence is exactly the prefix), 1 and a block edge."""
+    rng = np.random.default_rng(prefix_blocks + batch)
+    p_tok = prefix_blocks * block_size
+    suffix = [0, 1, block_size - 1, block_size, block_size + 1] + rng.integers(0, 600, batch - 5).tolist()
+    ctx = [p_tok + s for s in suffix]
+    b = workloads.build_batch(ctx, [1] * batch, n_q=n_q, n_kv=n_kv, head_dim=head_dim, block_size=block_size,
+                              dtype=dtype, device=device, seed=batch, pool_factor=1.3,
+                              shared_prefix_blocks=prefix_blocks)
+    out = _run(b, prefix_blocks)
+    assert_attn_close(out, _oracle(b), f"shared prefix {n_q}/{n_kv} D{head_dim} bs{block_size}")
+
+
+@pytest.mark.parametrize("n_q,n_kv,head_dim,block_size,batch,prefix_blocks", [
+    (28, 4, 128, 16, 2, 8),     # 14 rows per KV head: one decode tile, plain path
+    (8, 8, 256, 16, 24, 8),     # head_dim 256: plain path
+    (8, 8, 128, 8, 24, 16),     # 8-token blocks: plain path
+    (28, 4, 128, 16, 24, 0),    # no shared prefix
+])
+def test_plain_path_cases(device, n_q, n_kv, head_dim, block_size, batch, prefix_blocks):
+    rng = np.random.default_rng(batch)
+    ctx = [prefix_blocks * block_size + int(s) for s in rng.integers(1, 300, batch)]
+    b = workloads.build_batch(ctx, [1] * batch, n_q=n_q, n_kv=n_kv, head_dim=head_dim, block_size=block_size,
+                              dtype=torch.bfloat16, device=device, seed=7, pool_factor=1.3,
+                              shared_prefix_blocks=prefix_blocks)
+    out = _run(b, prefix_blocks)
+    assert_attn_close(out, _oracle(b), "plain path")
+
+
+def test_repeat_calls_are_identical_and_graph_replays(device):
+    """Deterministic: the prefix pass's item order does not change any result bit; a
+    captured call replays to the eager result."""
+    b = workloads.prefix_share(device=device, seed=9, batch=48)
+    first = _run(b, b.shared_blocks)
+    assert torch.equal(first, _run(b, b.shared_blocks))
+    q = b.padded_q().clone()
+    _run(b, b.shared_blocks)  # workspace size cached before capture
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = paged_attention_shared_prefix(q, b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16,
+                                            b.shared_blocks)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, first)
+
+
+def test_rejects_bad_prefix(device):
+    b = workloads.prefix_share(device=device, seed=1, batch=4)
+    with pytest.raises(ValueError, match="prefix_blocks"):
+        _run(b, b.block_tables.shape[1] + 1)
+    with pytest.raises(ValueError, match="q must be"):
+        paged_attention_shared_prefix(b.padded_q().expand(-1, -1, 2, -1), b.kv_cache, b.block_tables,
+                                      b.context_lens, 0, b.scale, 16, 4)
