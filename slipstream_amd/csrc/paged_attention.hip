@@ -10,8 +10,9 @@ int64_t decode_workspace_bytes(int dtype, int head_dim, int n_q, int n_kv, int m
 int launch_decode(const AttnParams& p, int dtype, int head_dim, int max_query_len, char* ws,
                   int64_t ws_bytes, hipStream_t stream);
 int64_t prefill_work_bytes(int64_t batch, int n_rep, int max_query_len);
+// planned: work already holds the list (count, then (b << 16) | query tile per entry)
 int launch_prefill(const AttnParams& p, int dtype, int head_dim, int max_query_len, int* work,
-                   int64_t work_bytes, hipStream_t stream);
+                   int64_t work_bytes, hipStream_t stream, bool planned);
 }  // namespace ss
 
 namespace {
@@ -96,7 +97,7 @@ int run(AttnParams& p, int dtype, int head_dim, int max_query_len, void* workspa
   auto prefill = [&](hipStream_t s) {
     const bool has_list = workspace && ws_bytes > dec_bytes;
     return ss::launch_prefill(p, dtype, head_dim, max_query_len, has_list ? (int*)((char*)workspace + dec_bytes) : nullptr,
-                              has_list ? ws_bytes - dec_bytes : 0, s);
+                              has_list ? ws_bytes - dec_bytes : 0, s, false);
   };
   // A packed step has both kinds of rows. They run one after the other, the prefill
   // first: each kernel fills every CU with one workgroup (registers, LDS), and the
@@ -293,17 +294,21 @@ PrefixPlan prefix_plan(int64_t batch, int n_q, int n_kv, int head_dim, int block
   return pl;
 }
 
-// meta = [cu: S + 1][chunk lengths: S][suffix lengths: batch][chunk tables: S * cb]
+// meta = [cu: S + 1][chunk lengths: S][suffix lengths: batch][chunk tables: S * cb];
+// work = the prefill's work list: every (chunk, query tile) item costs about the same
+// (the last chunk may be shorter), so it is written in order, without the cost sort
 __global__ __launch_bounds__(256) void prefix_setup_kernel(const int32_t* __restrict__ bt,
                                                            const int32_t* __restrict__ seq_lens, int batch, int S,
-                                                           int cb, int prefix_blocks, int block_size,
-                                                           int32_t* __restrict__ meta) {
+                                                           int cb, int prefix_blocks, int block_size, int qtiles,
+                                                           int32_t* __restrict__ meta, int32_t* __restrict__ work) {
   int32_t* cu = meta;
   int32_t* pctx = cu + S + 1;
   int32_t* sctx = pctx + S;
   int32_t* ptab = sctx + batch;
-  const int n = max(max(S + 1, batch), S * cb);
+  const int n = max(max(S + 1, batch), max(S * cb, S * qtiles + 1));
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    if (i == 0) work[0] = S * qtiles;
+    if (i < S * qtiles) work[1 + i] = ((i / qtiles) << 16) | (i % qtiles);
     if (i <= S) cu[i] = i * batch;
     if (i < S) pctx[i] = min(cb, prefix_blocks - i * cb) * block_size;
     if (i < batch) sctx[i] = max(seq_lens[i] - prefix_blocks * block_size, 0);
@@ -341,23 +346,48 @@ __global__ __launch_bounds__(256) void prefix_combine_kernel(const T* __restrict
     const int64_t bh = u / dv;
     const int b = (int)(bh / n_q), hq = (int)(bh - (int64_t)b * n_q);
     T* o = out + b * o_sb + hq * o_sh + 8 * c;
+    // running (max, weight sum, weighted output) from the suffix part; an empty suffix
+    // (lse -inf) starts from nothing. Every chunk holds at least one key, so the max is
+    // finite after the first batch and a -inf part weighs exactly 0.
     const float ls = sfx_lse[bh];
-    float mx = ls;
-    for (int s = 0; s < S; ++s) mx = fmaxf(mx, part_lse[s * rows + bh]);
-    // every chunk holds at least one key, so mx is finite; a -inf part weighs 0
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    float wsum = 0.f;
-    auto add = [&](const u32x4 v, float lse) {
-      const float w = fast_exp2(lse - mx);
-      wsum += w;
+    const bool has_sfx = ls > -__builtin_inff();
+    const u32x4 vs = load16(o);
+    float acc[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[2 * e] += w * half_to_f32<T>(v[e], 0);
-        acc[2 * e + 1] += w * half_to_f32<T>(v[e], 1);
+    for (int e = 0; e < 4; ++e) {
+      acc[2 * e] = has_sfx ? half_to_f32<T>(vs[e], 0) : 0.f;
+      acc[2 * e + 1] = has_sfx ? half_to_f32<T>(vs[e], 1) : 0.f;
+    }
+    float m = ls, wsum = has_sfx ? 1.f : 0.f;
+    // prefix parts four at a time: all loads of a batch issued before any is used
+    for (int s0 = 0; s0 < S; s0 += 4) {
+      float lv[4];
+      u32x4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t i = (int64_t)min(s0 + j, S - 1) * rows + bh;
+        lv[j] = part_lse[i];
+        v[j] = load16(part + i * head_dim + 8 * c);
       }
-    };
-    add(load16(o), ls);
-    for (int s = 0; s < S; ++s) add(load16(part + (s * rows + bh) * head_dim + 8 * c), part_lse[s * rows + bh]);
+      float mx = m;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) mx = s0 + j < S ? fmaxf(mx, lv[j]) : mx;
+      const float keep = fast_exp2(m - mx);
+      wsum *= keep;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] *= keep;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float w = s0 + j < S ? fast_exp2(lv[j] - mx) : 0.f;
+        wsum += w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[2 * e] += w * half_to_f32<T>(v[j][e], 0);
+          acc[2 * e + 1] += w * half_to_f32<T>(v[j][e], 1);
+        }
+      }
+      m = mx;
+    }
     const float inv = 1.f / wsum;
     store16(o, u32x4{Elem<T>::pack2(acc[0] * inv, acc[1] * inv), Elem<T>::pack2(acc[2] * inv, acc[3] * inv),
                      Elem<T>::pack2(acc[4] * inv, acc[5] * inv), Elem<T>::pack2(acc[6] * inv, acc[7] * inv)});
@@ -443,10 +473,13 @@ extern "C" int ss_paged_attention_shared_prefix(const void* q, void* out, const 
   float* lse = (float*)(ws + pl.dec + pl.work + pl.meta);
   void* part = ws + pl.dec + pl.work + pl.meta + pl.lse;
   const int64_t rows = batch * n_q;
+  int32_t* work = (int32_t*)(ws + pl.dec);
+  const int qtiles = (int)((batch * p.n_rep + 127) / 128);
   {
-    const int n = std::max<int64_t>(std::max<int64_t>(pl.S + 1, batch), (int64_t)pl.S * pl.cb);
-    hipLaunchKernelGGL(prefix_setup_kernel, dim3((n + 255) / 256), dim3(256), 0, s, block_tables, seq_lens,
-                       (int)batch, pl.S, pl.cb, prefix_blocks, block_size, meta);
+    const int64_t n = std::max<int64_t>(std::max<int64_t>(pl.S + 1, batch),
+                                        std::max<int64_t>((int64_t)pl.S * pl.cb, (int64_t)pl.S * qtiles + 1));
+    hipLaunchKernelGGL(prefix_setup_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, block_tables,
+                       seq_lens, (int)batch, pl.S, pl.cb, prefix_blocks, block_size, qtiles, meta, work);
     if ((st = ss_host::launch_status("shared-prefix setup")) != SS_OK) return st;
   }
   const int32_t* cu = meta;
@@ -468,7 +501,7 @@ extern "C" int ss_paged_attention_shared_prefix(const void* q, void* out, const 
     pp.lse = lse;
     pp.noncausal = 1;
     pp.q_period = (int)batch;
-    st = ss::launch_prefill(pp, dtype, head_dim, (int)batch, (int*)(ws + pl.dec), pl.work, s);
+    st = ss::launch_prefill(pp, dtype, head_dim, (int)batch, work, pl.work, s, true);
     if (st != SS_OK) return st;
   }
   {  // 2. private suffixes: the table from column prefix_blocks on

@@ -800,7 +800,7 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const AttnParams p, 
 constexpr int kPrefillNT = 2;
 
 template <typename T, int D>
-int launch_prefill_typed(const AttnParams& p, int max_query_len, int* work, int64_t work_bytes,
+int launch_prefill_typed(const AttnParams& p, int max_query_len, int* work, int64_t work_bytes, bool planned,
                          hipStream_t stream) {
   if (D <= 128 && p.block_size >= 16) {
     constexpr int rows = 128;
@@ -828,9 +828,11 @@ int launch_prefill_typed(const AttnParams& p, int max_query_len, int* work, int6
       }
       attr_set = true;
     }
-    hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPlanBuckets), 0, stream, p, work, (int)qtiles);
-    int st = ss_host::launch_status("paged attention prefill plan");
-    if (st != SS_OK) return st;
+    if (!planned) {
+      hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPlanBuckets), 0, stream, p, work, (int)qtiles);
+      int st = ss_host::launch_status("paged attention prefill plan");
+      if (st != SS_OK) return st;
+    }
     // one resident workgroup per CU (the LDS rings take 96 KB); never more than items
     const int64_t items = (int64_t)p.batch * qtiles * p.n_kv;
     const int64_t cus = ss_host::device_cu_count();
@@ -862,15 +864,15 @@ int64_t prefill_work_bytes(int64_t batch, int n_rep, int max_query_len) {
 }
 
 int launch_prefill(const AttnParams& p, int dtype, int head_dim, int max_query_len, int* work,
-                   int64_t work_bytes, hipStream_t stream) {
+                   int64_t work_bytes, hipStream_t stream, bool planned) {
   if (dtype == SS_DTYPE_BF16) {
-    if (head_dim == 64) return launch_prefill_typed<bf16_t, 64>(p, max_query_len, work, work_bytes, stream);
-    if (head_dim == 128) return launch_prefill_typed<bf16_t, 128>(p, max_query_len, work, work_bytes, stream);
-    return launch_prefill_typed<bf16_t, 256>(p, max_query_len, work, work_bytes, stream);
+    if (head_dim == 64) return launch_prefill_typed<bf16_t, 64>(p, max_query_len, work, work_bytes, planned, stream);
+    if (head_dim == 128) return launch_prefill_typed<bf16_t, 128>(p, max_query_len, work, work_bytes, planned, stream);
+    return launch_prefill_typed<bf16_t, 256>(p, max_query_len, work, work_bytes, planned, stream);
   }
-  if (head_dim == 64) return launch_prefill_typed<f16_t, 64>(p, max_query_len, work, work_bytes, stream);
-  if (head_dim == 128) return launch_prefill_typed<f16_t, 128>(p, max_query_len, work, work_bytes, stream);
-  return launch_prefill_typed<f16_t, 256>(p, max_query_len, work, work_bytes, stream);
+  if (head_dim == 64) return launch_prefill_typed<f16_t, 64>(p, max_query_len, work, work_bytes, planned, stream);
+  if (head_dim == 128) return launch_prefill_typed<f16_t, 128>(p, max_query_len, work, work_bytes, planned, stream);
+  return launch_prefill_typed<f16_t, 256>(p, max_query_len, work, work_bytes, planned, stream);
 }
 
 }  // namespace ss
