@@ -81,6 +81,7 @@ def test_shapes_and_empty_suffixes(device, dtype, n_q, n_kv, head_dim, block_siz
     (8, 8, 256, 16, 24, 8),     # head_dim 256: plain path
     (8, 8, 128, 8, 24, 16),     # 8-token blocks: plain path
     (28, 4, 128, 16, 24, 0),    # no shared prefix
+    (32, 1, 128, 16, 6, 8),     # 32 query heads per KV head: the prefill kernel's plain path
 ])
 def test_plain_path_cases(device, n_q, n_kv, head_dim, block_size, batch, prefix_blocks):
     rng = np.random.default_rng(batch)
