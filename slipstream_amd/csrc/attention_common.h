@@ -38,6 +38,7 @@ struct AttnParams {
   float* lse;     // when set, log2-domain log-sum-exp of each query row: [tokens, n_q]
   int noncausal;  // every query row sees all of its sequence's keys
   int q_period;   // when > 0, query token t is read from row t % q_period
+  int range_cap;  // when > 0, at most this many decode ranges per head group
 };
 
 // Decode tile: one wave covers up to 16 query rows (query token j, head i in

@@ -791,6 +791,11 @@ static int launch_decode_typed(AttnParams p, int max_query_len, char* ws, int64_
   p.hpw = g.hpw;
   p.n_hgroups = g.n_hgroups;
   p.n_ranges = g.n_ranges;
+  int n_wg = g.n_wg;  // fewer ranges than the geometry's use a prefix of its workspace
+  if (p.range_cap > 0 && p.n_ranges > p.range_cap) {
+    p.n_ranges = p.range_cap;
+    n_wg = p.n_ranges * g.n_hgroups;
+  }
   if (p.rmax != g.rmax) {
     ss_host::set_error("paged attention: decode row split %d != geometry %d", p.rmax, g.rmax);
     return SS_ERR_INVALID;
@@ -801,16 +806,16 @@ static int launch_decode_typed(AttnParams p, int max_query_len, char* ws, int64_
   // default cache policy, so pages shared between sequences are re-read from it.
   const int64_t pool_bytes = 2 * (int64_t)p.num_blocks * p.c_sb * (int64_t)sizeof(T);
   if (p.block_size >= 16 && D <= 128 && pool_bytes > kMallReuseBytes)
-    hipLaunchKernelGGL((decode_kernel<T, D, true, kNonTemporal>), dim3(g.n_wg), dim3(g.hpw * 64), 0, stream, p);
+    hipLaunchKernelGGL((decode_kernel<T, D, true, kNonTemporal>), dim3(n_wg), dim3(g.hpw * 64), 0, stream, p);
   else if (p.block_size >= 16 && D <= 128)
-    hipLaunchKernelGGL((decode_kernel<T, D, true, kDefaultPolicy>), dim3(g.n_wg), dim3(g.hpw * 64), 0, stream,
+    hipLaunchKernelGGL((decode_kernel<T, D, true, kDefaultPolicy>), dim3(n_wg), dim3(g.hpw * 64), 0, stream,
                        p);
   else
-    hipLaunchKernelGGL((decode_kernel<T, D, false, kDefaultPolicy>), dim3(g.n_wg), dim3(g.hpw * 64), 0, stream,
+    hipLaunchKernelGGL((decode_kernel<T, D, false, kDefaultPolicy>), dim3(n_wg), dim3(g.hpw * 64), 0, stream,
                        p);
   int st = ss_host::launch_status("paged attention decode");
   if (st != SS_OK) return st;
-  hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(g.n_wg + p.batch), dim3(256), 0, stream, p, g.n_wg);
+  hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(n_wg + p.batch), dim3(256), 0, stream, p, n_wg);
   return ss_host::launch_status("paged attention decode merge");
 }
 
