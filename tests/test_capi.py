@@ -158,3 +158,41 @@ def test_attention_workspace_holds_the_prefill_work_list():
                                 q_str, o_str, c_str, 64, 1.0, _ffi.SS_DTYPE_BF16, fake, size(4, 1), None)
     assert st == _ffi.SS_ERR_WORKSPACE, lib.ss_last_error()
     assert b"work list" in lib.ss_last_error()
+
+
+def test_shared_prefix_argument_errors_need_no_device():
+    """The shared-prefix entry checks GQA, batch and prefix_blocks on the host; an empty
+    batch returns SS_OK before any HIP call; the Python wrapper refuses CPU tensors."""
+    import torch
+
+    from slipstream_amd import _ffi
+    from slipstream_amd.kernels import paged_attention_shared_prefix
+
+    lib = _ffi.lib()
+    out = ctypes.c_int64(0)
+    bf16 = _ffi.SS_DTYPE_BF16
+    size = lib.ss_paged_attention_shared_prefix_workspace_size
+    assert size(-1, 28, 4, 128, 16, 8, bf16, ctypes.byref(out)) == _ffi.SS_ERR_INVALID
+    assert size(4, 28, 4, 128, 16, -1, bf16, ctypes.byref(out)) == _ffi.SS_ERR_INVALID
+    assert size(4, 6, 4, 128, 16, 8, bf16, ctypes.byref(out)) == _ffi.SS_ERR_INVALID
+    z2, z3 = _ffi.i64_array([0, 0]), _ffi.i64_array([0, 0, 0])
+
+    def call(batch, n_q, n_kv, max_blocks, prefix_blocks):
+        return lib.ss_paged_attention_shared_prefix(None, None, None, None, None, None, batch, n_q, n_kv, 128,
+                                                    max_blocks, 16, 64, prefix_blocks, z2, z2, z3, max_blocks,
+                                                    1.0, bf16, None, 0, None)
+
+    assert call(4, 28, 4, 8, 9) == _ffi.SS_ERR_INVALID
+    assert b"prefix_blocks" in lib.ss_last_error()
+    assert call(4, 28, 4, 8, -1) == _ffi.SS_ERR_INVALID
+    assert call(4, 6, 4, 8, 2) == _ffi.SS_ERR_INVALID
+    assert b"GQA" in lib.ss_last_error()
+    assert call(0, 28, 4, 8, 2) == _ffi.SS_OK
+    q = torch.zeros(4, 28, 1, 128, dtype=torch.bfloat16)
+    kv = torch.zeros(1, 2, 64, 16, 4, 128, dtype=torch.bfloat16)
+    bt = torch.zeros(4, 8, dtype=torch.int32)
+    lens = torch.full((4,), 64, dtype=torch.int32)
+    with pytest.raises(ValueError, match="prefix_blocks"):
+        paged_attention_shared_prefix(q, kv, bt, lens, 0, 0.1, 16, 9)
+    with pytest.raises(RuntimeError, match="HIP devices only"):
+        paged_attention_shared_prefix(q, kv, bt, lens, 0, 0.1, 16, 2)
