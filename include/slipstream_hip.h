@@ -121,6 +121,22 @@ int ss_paged_attention_varlen(const void* q, void* out, const void* k_cache, con
                               int64_t workspace_bytes, void* stream);
 
 /*
+ * Device status word of the current GPU, OR-ed by the attention kernels when a
+ * packed description breaks the caller's promises (SS_STATUS_* bits):
+ *   SS_STATUS_QUERY_TOO_LONG  a sequence of ss_paged_attention_varlen had more query
+ *     tokens than max_query_len covers; its uncovered rows were written as zeros;
+ *   SS_STATUS_STREAM_OVERRUN  cu_seqlens ran past total_tokens (or backwards); the
+ *     kernels clamped every sequence into [0, total_tokens).
+ * The reference raises ValueError at such inputs (slipstream/models/layers/attention.py:44-45);
+ * a device kernel cannot, so it writes defined values and reports here. Waits for
+ * `stream`, then stores the word in *flags and clears it when `clear` is nonzero.
+ * No counterpart in the reference (its checks are synchronous host code).
+ */
+#define SS_STATUS_QUERY_TOO_LONG 1
+#define SS_STATUS_STREAM_OVERRUN 2
+int ss_attention_status(int* flags, int clear, void* stream);
+
+/*
  * Decode (one query token per sequence) for a batch whose block tables all begin
  * with the same prefix_blocks physical blocks, the tables a prefix-cache hit
  * produces (RadixPrefixCache.match / attach: slipstream/memory/prefix_cache.py:37-56,
@@ -250,7 +266,9 @@ int ss_rope_and_cache(const void* q, const void* k, const void* v, const void* c
  *     p = prior_lens[b] + j) -> table[b][p / block_size] * block_size + p % block_size,
  *     the slot BlockManagerImpl.append_slot hands out when earlier blocks are full
  *     (block_manager.py:141-159); -1 past the table or on a negative entry.
- * Negative lengths count as 0; tokens past total_tokens are not written. Nothing
+ * Negative lengths count as 0; tokens past total_tokens are not written, and entries
+ * [sum(query_lens), total_tokens) of slot_mapping are set to -1 (skipped by the
+ * scatter), so an over-sized slot_mapping never holds a stale slot. Nothing
  * is read back to the host, so a step built this way can be graph-captured.
  */
 int ss_build_step_metadata(const int32_t* block_tables, int64_t bt_stride, int max_blocks,

@@ -60,12 +60,15 @@ def reshape_and_cache(
         kv_cache[layer_idx, 1, s // block_size, s % block_size] = v[n]
 
 
-def build_step_metadata(tables: list[list[int]], prior_lens, query_lens, block_size: int):
+def build_step_metadata(tables: list[list[int]], prior_lens, query_lens, block_size: int,
+                        total_tokens: int | None = None):
     """Packed metadata of one step (paged_cache.py:71-109 with the packed description):
     ``cu_seqlens`` = [0] + cumsum(query_lens), ``context_lens`` = prior + query, and the
     slot of token j of sequence b at position p = prior[b] + j:
     ``tables[b][p // bs] * bs + p % bs`` (-1 past the table or on a negative entry).
-    Negative lengths count as 0."""
+    Negative lengths count as 0. With ``total_tokens`` the slot list has exactly that
+    many entries: cut after it, or padded with -1 (one slot per new token,
+    paged_cache.py:85-109; a padded entry names no token, so the scatter skips it)."""
     q = [max(int(v), 0) for v in query_lens]
     p0 = [max(int(v), 0) for v in prior_lens]
     cu = [0]
@@ -79,6 +82,8 @@ def build_step_metadata(tables: list[list[int]], prior_lens, query_lens, block_s
             e = table[bi] if bi < len(table) else -1
             slots.append(e * block_size + pos % block_size if e >= 0 else -1)
     ctx = [a + b for a, b in zip(p0, q)]
+    if total_tokens is not None:
+        slots = (slots + [-1] * total_tokens)[:total_tokens]
     return np.array(cu, np.int32), np.array(ctx, np.int32), np.array(slots, np.int64)
 
 
@@ -135,20 +140,23 @@ def attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, valid: np.ndarray, seq_l
     out = np.zeros((tq, n_q, d), dtype=np.float64)
     if s == 0 or tq == 0:
         return out
-    kh = k[:, np.arange(n_q) // n_rep, :].transpose(1, 0, 2)  # [n_q, S, D]
-    vh = v[:, np.arange(n_q) // n_rep, :].transpose(1, 0, 2)
-    scores = np.einsum("hjd,hsd->hjs", q.astype(np.float64), kh.astype(np.float64)) * scale
+    # query head h = g * n_rep + r reads KV head g (repeat_kv): the n_rep heads of a
+    # group share one batched product with their KV head, [n_kv, n_rep * Tq, S]
+    qg = q.astype(np.float64).reshape(n_kv, n_rep * tq, d)
+    kg = np.ascontiguousarray(k.transpose(1, 0, 2), dtype=np.float64)  # [n_kv, S, D]
+    vg = np.ascontiguousarray(v.transpose(1, 0, 2), dtype=np.float64)
+    scores = np.matmul(qg, kg.transpose(0, 2, 1)).reshape(n_kv, n_rep, tq, s) * scale
     key_pos = np.arange(s)[None, :]
     query_abs = (seq_len - tq + np.arange(tq))[:, None]
-    visible = (key_pos <= query_abs) & valid[None, :]
-    scores = np.where(visible[None], scores, -np.inf)
+    visible = (key_pos <= query_abs) & valid[None, :]  # [Tq, S]
+    scores = np.where(visible, scores, -np.inf)
     m = scores.max(axis=-1, keepdims=True)
     any_vis = np.isfinite(m)
-    p = np.where(visible[None], np.exp(scores - np.where(any_vis, m, 0.0)), 0.0)
+    p = np.where(visible, np.exp(scores - np.where(any_vis, m, 0.0)), 0.0)
     denom = p.sum(axis=-1, keepdims=True)
     w = np.where(denom > 0, p / np.where(denom > 0, denom, 1.0), 0.0)
-    o = np.einsum("hjs,hsd->hjd", w, vh.astype(np.float64))  # [n_q, Tq, D]
-    return o.transpose(1, 0, 2)
+    o = np.matmul(w.reshape(n_kv, n_rep * tq, s), vg)  # [n_kv, n_rep * Tq, D]
+    return o.reshape(n_q, tq, d).transpose(1, 0, 2)
 
 
 def paged_attention(

@@ -4,8 +4,15 @@ This is what slipstream runs when its fast path is off or absent: a Python
 loop over the batch, a gather of each sequence's pages into contiguous K/V,
 ``repeat_kv``, bf16/fp16 matmuls with a float32 softmax, and for W4A16 a full
 dequantised weight then a dense matmul. ``bench.py`` times it on the host as
-the CPU baseline; tests use it as the dtype-faithful secondary check. It
-restates (not imports) the reference:
+the CPU baseline, and the GPU tests report the HIP kernels' distance to it as
+the dtype-faithful secondary check. Its own pins (tests/test_oracle_reference_path.py):
+the scatter bit for bit against ``oracle.paged_attention.reshape_and_cache``; the
+gather's copy, truncation and negative-index hole rule in closed form; attention in
+float32 against the float64 oracle and torch's SDPA (1e-5), and in bf16/fp16 within
+those dtypes' rounding bounds; W4A16 against the oracle's dequantise-then-matmul.
+Where the reference and the HIP path's chosen semantics differ (holes in a table,
+a query longer than its keys) this module keeps the reference's behaviour.
+It restates (not imports) the reference:
   gather          slipstream/kernels/attention_ref.py:42-65
   eager attention slipstream/models/layers/attention.py:20-88
   paged loop      slipstream/kernels/attention_ref.py:68-89
@@ -20,7 +27,17 @@ import torch
 
 def scatter(k: torch.Tensor, v: torch.Tensor, kv: torch.Tensor, slots: torch.Tensor, layer: int,
             block_size: int) -> None:
-    """index_put of ``[N, n_kv, D]`` rows at ``(slot // bs, slot % bs)``."""
+    """index_put of ``[N, n_kv, D]`` (or ``[B, n_kv, T, D]``, token b*T + t) rows at
+    ``(slot // bs, slot % bs)``; a negative slot indexes from the end, as in the reference."""
+    if k.shape != v.shape:
+        raise ValueError(f"k/v shape mismatch {tuple(k.shape)} vs {tuple(v.shape)}")
+    if k.ndim == 4:
+        k = k.permute(0, 2, 1, 3).reshape(-1, k.shape[1], k.shape[3])
+        v = v.permute(0, 2, 1, 3).reshape(-1, v.shape[1], v.shape[3])
+    if slots.numel() != k.shape[0]:
+        raise ValueError(f"slot_mapping {slots.numel()} != tokens {k.shape[0]}")
+    if k.shape[0] == 0:
+        return
     blk = torch.div(slots, block_size, rounding_mode="floor")
     off = slots % block_size
     kv[layer, 0, blk, off] = k
@@ -28,7 +45,9 @@ def scatter(k: torch.Tensor, v: torch.Tensor, kv: torch.Tensor, slots: torch.Ten
 
 
 def gather(kv: torch.Tensor, layer: int, table: torch.Tensor, seq_len: int, block_size: int):
-    """One sequence's pages -> contiguous ``[1, n_kv, S, D]`` K and V."""
+    """One sequence's pages -> contiguous ``[1, n_kv, S, D]`` K and V: the first
+    ``min(ceil(seq_len / bs), #entries >= 0)`` table entries, so a short table truncates
+    the keys and a -1 inside that range reads the pool's last block (Python indexing)."""
     valid = int((table >= 0).sum().item()) if table.numel() else 0
     n_blocks = min((seq_len + block_size - 1) // block_size, valid)
     n_kv, d = kv.shape[4], kv.shape[5]
@@ -49,6 +68,8 @@ def eager(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float) -> to
         k = k[:, :, None].expand(b, h, n_rep, s, d).reshape(b, h * n_rep, s, d)
         v = v[:, :, None].expand(b, h, n_rep, s, d).reshape(b, h * n_rep, s, d)
     tq, s = q.shape[2], k.shape[2]
+    if tq > s:  # packed_causal_mask, attention.py:44-45
+        raise ValueError(f"query_len {tq} > key_len {s}")
     scores = torch.matmul(q, k.transpose(2, 3)) * scale
     key_pos = torch.arange(s)
     q_abs = torch.arange(s - tq, s)

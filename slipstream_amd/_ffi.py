@@ -22,6 +22,9 @@ SS_ERR_UNSUPPORTED = 2
 SS_ERR_LAUNCH = 3
 SS_ERR_WORKSPACE = 4
 
+SS_STATUS_QUERY_TOO_LONG = 1
+SS_STATUS_STREAM_OVERRUN = 2
+
 SS_DTYPE_F16 = 0
 SS_DTYPE_BF16 = 1
 SS_DTYPE_F32 = 2
@@ -47,6 +50,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _c_i64p, _c_i64p, _c_i64p, _i64, ctypes.c_float, _i32, _vp, _i64, _vp,
         ],
     ),
+    "ss_attention_status": (_i32, [ctypes.POINTER(ctypes.c_int), _i32, _vp]),
     "ss_paged_attention_shared_prefix_workspace_size": (_i32, [_i64, _i32, _i32, _i32, _i32, _i32, _i32, _c_i64p]),
     "ss_paged_attention_shared_prefix": (
         _i32,

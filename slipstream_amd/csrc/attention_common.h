@@ -39,7 +39,21 @@ struct AttnParams {
   int noncausal;  // every query row sees all of its sequence's keys
   int q_period;   // when > 0, query token t is read from row t % q_period
   int range_cap;  // when > 0, at most this many decode ranges per head group
+  // Packed form only: query tokens in q/out. cu_seqlens entries are clamped into
+  // [0, total_tokens], so a stream description that runs past q never indexes
+  // outside it.
+  int total_tokens;
+  // Query rows per (sequence, KV head) the prefill launch of this call covers
+  // (query tiles x rows per tile; 0 when no prefill runs). Rows of a longer
+  // sequence (a query longer than the call's max_query_len) are written as zeros
+  // by the decode merge, which also raises kStatusQueryTooLong.
+  int row_cap;
 };
+
+// Bits of the device status word (ss_attention_status): set by kernels that met a
+// packed description they could not compute, never cleared by them.
+constexpr int kStatusQueryTooLong = 1;   // qlen > max_query_len: rows zero-filled
+constexpr int kStatusStreamOverrun = 2;  // cu_seqlens beyond total_tokens: clamped
 
 // Decode tile: one wave covers up to 16 query rows (query token j, head i in
 // the GQA group) of one KV head; r = j * n_rep + i.
@@ -49,8 +63,9 @@ constexpr int kPairTokens = 32;
 
 __device__ __forceinline__ void seq_queries(const AttnParams& p, int b, int& qlen, int64_t& qoff) {
   if (p.cu) {
-    const int s = p.cu[b];
-    qlen = p.cu[b + 1] - s;
+    const int s = min(max(p.cu[b], 0), p.total_tokens);
+    const int e = min(max(p.cu[b + 1], s), p.total_tokens);
+    qlen = e - s;
     qoff = s;
   } else {
     qlen = p.tq;

@@ -10,9 +10,11 @@ int64_t decode_workspace_bytes(int dtype, int head_dim, int n_q, int n_kv, int m
 int launch_decode(const AttnParams& p, int dtype, int head_dim, int max_query_len, char* ws,
                   int64_t ws_bytes, hipStream_t stream);
 int64_t prefill_work_bytes(int64_t batch, int n_rep, int max_query_len);
+int64_t prefill_row_cap(int n_rep, int max_query_len);
 // planned: work already holds the list (count, then (b << 16) | query tile per entry)
 int launch_prefill(const AttnParams& p, int dtype, int head_dim, int max_query_len, int* work,
                    int64_t work_bytes, hipStream_t stream, bool planned);
+int read_status(int* flags, int clear, hipStream_t stream);
 }  // namespace ss
 
 namespace {
@@ -80,6 +82,8 @@ void fill_common(AttnParams& p, const void* q, void* out, const void* k_cache, c
   p.block_size = block_size;
   p.bs_shift = __builtin_ctz((unsigned)block_size);
   p.scale_log2 = scale * ss::kLog2e;
+  p.total_tokens = 0x7fffffff;
+  p.row_cap = 0;
 }
 
 // Workspace layout: [decode split-K partials, 256-byte aligned][prefill work list].
@@ -90,6 +94,7 @@ int64_t decode_part_bytes(int dtype, int head_dim, int n_q, int n_kv, int max_qu
 int run(AttnParams& p, int dtype, int head_dim, int max_query_len, void* workspace, int64_t ws_bytes,
         hipStream_t stream, bool decode_rows, bool prefill_rows) {
   p.rmax = ss::decode_rows_for(max_query_len, p.n_rep);
+  p.row_cap = prefill_rows ? (int)std::min<int64_t>(ss::prefill_row_cap(p.n_rep, max_query_len), 0x7fffffff) : 0;
   const int64_t dec_bytes = decode_part_bytes(dtype, head_dim, p.n_q, p.n_kv, max_query_len);
   auto decode = [&](hipStream_t s) {
     return ss::launch_decode(p, dtype, head_dim, max_query_len, (char*)workspace, ws_bytes, s);
@@ -193,9 +198,12 @@ extern "C" int ss_paged_attention_varlen(const void* q, void* out, const void* k
     ss_host::set_error("%s: negative batch, token count or max_query_len", who);
     return SS_ERR_INVALID;
   }
-  if (batch == 0 || total_tokens == 0 || max_query_len == 0) return SS_OK;
-  if (batch > 0x7fffffff) {
-    ss_host::set_error("%s: batch %lld too large", who, (long long)batch);
+  // max_query_len == 0 with tokens present breaks the caller's promise like any
+  // other short max_query_len: the decode merge zero-fills such rows and flags them
+  if (batch == 0 || total_tokens == 0) return SS_OK;
+  if (batch > 0x7fffffff || total_tokens > 0x7fffffff) {
+    ss_host::set_error("%s: batch %lld or token count %lld too large (int32 cu_seqlens)", who, (long long)batch,
+                       (long long)total_tokens);
     return SS_ERR_UNSUPPORTED;
   }
   if ((st = check_strides(who, q_strides, 2)) != SS_OK) return st;
@@ -213,6 +221,7 @@ extern "C" int ss_paged_attention_varlen(const void* q, void* out, const void* k
   fill_common(p, q, out, k_cache, v_cache, block_tables, context_lens, batch, n_q, n_kv, max_blocks,
               block_size, num_blocks, c_strides, bt_stride, scale);
   p.cu = cu_seqlens;
+  p.total_tokens = (int)total_tokens;
   p.tq = 0;
   p.q_sb = 0;
   p.q_st = q_strides[0];
@@ -530,4 +539,14 @@ extern "C" int ss_paged_attention_shared_prefix(const void* q, void* out, const 
                        lse + (int64_t)pl.S * rows, (f16_t*)out, o_strides[0], o_strides[1], (int)batch, n_q,
                        head_dim, pl.S);
   return ss_host::launch_status("shared-prefix combine");
+}
+
+extern "C" int ss_attention_status(int* flags, int clear, void* stream) {
+  if (!flags) {
+    ss_host::set_error("attention status: null output pointer");
+    return SS_ERR_INVALID;
+  }
+  const int st = ss::read_status(flags, clear, (hipStream_t)stream);
+  if (st != SS_OK) ss_host::set_error("attention status: %s", hipGetErrorString(hipGetLastError()));
+  return st;
 }

@@ -36,6 +36,10 @@ namespace {
 // table entry is negative or out of range). Never written, so it stays zero.
 __device__ __attribute__((aligned(16))) uint32_t g_zero_row[128];
 
+// Device status word of this GPU (kStatus* bits), read and cleared by
+// ss_attention_status. Kernels only OR bits into it.
+__device__ int g_status;
+
 __device__ __forceinline__ int block_sum(int v, int* sh) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
@@ -624,8 +628,14 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
 }
 
 // Combine the partials of every sequence cut by a range boundary (blocks
-// [0, n_wg)), and write zeros for decode sequences with no visible key
-// (blocks [n_wg, n_wg + batch)).
+// [0, n_wg)), and write the rows no attention kernel of the call writes (blocks
+// [n_wg, n_wg + batch), one per sequence):
+//  - a decode sequence with no visible key: zeros (the Triton rule, l == 0);
+//  - query rows past what this call's kernels cover, which only a packed stream
+//    whose sequence is longer than max_query_len has: zeros, and the status word
+//    gets kStatusQueryTooLong, so a broken promise never leaves rows unwritten.
+// A packed stream whose cu_seqlens run past total_tokens raises kStatusStreamOverrun
+// (seq_queries has clamped it).
 template <typename T, int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const AttnParams p, int n_wg) {
   const int tid = threadIdx.x;
@@ -634,12 +644,26 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const AttnParams p, i
     int qlen;
     int64_t qoff;
     seq_queries(p, b, qlen, qoff);
-    if (!is_decode_seq(p, qlen) || decode_pairs(p, b) != 0) return;
+    if (p.cu && tid == 0 && (p.cu[b + 1] > p.total_tokens || p.cu[b] > p.cu[b + 1] || p.cu[b] < 0))
+      atomicOr(&g_status, kStatusStreamOverrun);
+    if (qlen <= 0) return;
+    const int R = qlen * p.n_rep;
+    int covered;  // rows r = j * n_rep + i (per KV head) some kernel writes
+    if (is_decode_seq(p, qlen)) {
+      if (decode_pairs(p, b) != 0) return;
+      covered = 0;
+    } else {
+      covered = min(R, p.row_cap);
+      if (covered >= R) return;
+      if (tid == 0) atomicOr(&g_status, kStatusQueryTooLong);
+    }
+    const int j0 = covered / p.n_rep;
     const int64_t per_tok = (int64_t)p.n_q * D;
-    for (int64_t idx = tid; idx < (int64_t)qlen * per_tok; idx += blockDim.x) {
+    for (int64_t idx = (int64_t)j0 * per_tok + tid; idx < (int64_t)qlen * per_tok; idx += blockDim.x) {
       const int j = (int)(idx / per_tok);
       const int rem = (int)(idx - (int64_t)j * per_tok);
       const int hq = rem / D, d = rem - hq * D;
+      if (j * p.n_rep + hq % p.n_rep < covered) continue;
       T* o = (T*)p.out + (int64_t)b * p.o_sb + (qoff + j) * p.o_st + (int64_t)hq * p.o_sh + d;
       *o = (T)0.f;
       if (p.lse && d == 0) p.lse[lse_index(p, b, qoff, j, hq)] = -__builtin_inff();
@@ -817,6 +841,22 @@ static int launch_decode_typed(AttnParams p, int max_query_len, char* ws, int64_
   if (st != SS_OK) return st;
   hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(n_wg + p.batch), dim3(256), 0, stream, p, n_wg);
   return ss_host::launch_status("paged attention decode merge");
+}
+
+// Read (and optionally clear) this device's status word after the work queued on
+// `stream` has finished.
+int read_status(int* flags, int clear, hipStream_t stream) {
+  if (hipStreamSynchronize(stream) != hipSuccess) return SS_ERR_LAUNCH;
+  int v = 0;
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_status), sizeof(int), 0, hipMemcpyDeviceToHost) != hipSuccess)
+    return SS_ERR_LAUNCH;
+  if (clear && v != 0) {
+    const int zero = 0;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_status), &zero, sizeof(int), 0, hipMemcpyHostToDevice) != hipSuccess)
+      return SS_ERR_LAUNCH;
+  }
+  *flags = v;
+  return SS_OK;
 }
 
 int launch_decode(const AttnParams& p, int dtype, int head_dim, int max_query_len, char* ws,

@@ -857,6 +857,14 @@ int launch_prefill_typed(const AttnParams& p, int max_query_len, int* work, int6
 
 }  // namespace
 
+// Query rows per (sequence, KV head) a prefill launch for max_query_len covers: both
+// kernels cut the rows into 128-row query tiles.
+int64_t prefill_row_cap(int n_rep, int max_query_len) {
+  static_assert(PrefillCfg<bf16_t, 128, kPrefillNT>::ROWS == 128, "per-lane prefill tiles hold 128 rows");
+  const int64_t rows = (int64_t)(max_query_len < 1 ? 1 : max_query_len) * n_rep;
+  return (rows + 127) / 128 * 128;
+}
+
 int64_t prefill_work_bytes(int64_t batch, int n_rep, int max_query_len) {
   const int64_t rows = (int64_t)(max_query_len < 1 ? 1 : max_query_len) * n_rep;
   if (rows <= kDecodeRows) return 0;  // no prefill rows

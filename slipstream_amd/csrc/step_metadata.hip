@@ -11,7 +11,8 @@
 // which is the slot BlockManagerImpl.append_slot hands out for the token at position
 // p when the table's earlier blocks are full (block_manager.py:141-159,282-287:
 // tokens fill the first not-full block in table order). A position past the table or
-// on a negative entry gets slot -1 (the scatter skips it). With this, a step's
+// on a negative entry gets slot -1 (the scatter skips it), and so does every entry
+// of slot_mapping past the step's last token. With this, a step's
 // metadata needs no host lists, no uploads and no host synchronisation, so the step
 // can be captured in a graph and replayed with new lengths.
 //
@@ -55,6 +56,10 @@ __global__ __launch_bounds__(256) void step_metadata_kernel(const MetaArgs a) {
     a.ctx[b] = p0 + q;
     if (b == a.batch - 1) a.cu[a.batch] = (int32_t)(base + q);
   }
+  // a slot_mapping longer than the step's tokens: its tail must not hold stale slots,
+  // which the scatter would take for real ones and write other sequences' pages
+  if (b == a.batch - 1)
+    for (int64_t t = base + q + tid; t < a.total; t += 256) a.slots[t] = -1;
   const int32_t* row = a.tables + (int64_t)b * a.bt_stride;
   for (int j = tid; j < q; j += 256) {
     const int64_t t = base + j;

@@ -2,6 +2,7 @@
 
 from slipstream_amd.kernels.block_copy import copy_blocks, swap_blocks
 from slipstream_amd.kernels.paged_attention import (
+    attention_status,
     paged_attention,
     paged_attention_decode,
     paged_attention_prefill,
@@ -15,6 +16,7 @@ from slipstream_amd.kernels.reshape_and_cache import reshape_and_cache
 from slipstream_amd.kernels.rope_cache import rope_and_cache
 
 __all__ = [
+    "attention_status",
     "copy_blocks",
     "fused_rmsnorm",
     "fused_swiglu",

@@ -281,6 +281,37 @@ def paged_attention_prefill(
     return paged_attention(q, kv_cache, block_tables, seq_lens, layer_idx, scale, block_size)
 
 
+def _check_stream(cu: torch.Tensor, total: int, max_query_len: int) -> None:
+    """Host check of a packed description (reads ``cu_seqlens`` back: debug only).
+
+    The reference raises ``ValueError`` for queries it cannot attend
+    (``attention.py:44-45``); without this check the device kernels write zeros for
+    rows past ``max_query_len`` and clamp a stream that runs past ``q``, and report
+    both through :func:`attention_status`."""
+    c = cu.cpu()
+    lens = c[1:] - c[:-1]
+    if int(c[0]) < 0 or bool((lens < 0).any()):
+        raise ValueError("cu_seqlens must start at >= 0 and be non-decreasing")
+    if int(c[-1]) > total:
+        raise ValueError(f"cu_seqlens[-1] = {int(c[-1])} > {total} query tokens")
+    if lens.numel() and int(lens.max()) > max_query_len:
+        raise ValueError(f"query_len {int(lens.max())} > max_query_len {max_query_len}")
+
+
+def attention_status(device: torch.device | int | None = None, clear: bool = True) -> int:
+    """The device status word (``ss_attention_status``) after the current stream's work:
+    ``SS_STATUS_QUERY_TOO_LONG`` (a packed sequence longer than ``max_query_len``, its
+    extra rows written as zeros) and ``SS_STATUS_STREAM_OVERRUN`` (``cu_seqlens`` past
+    the token count, clamped). Synchronises the stream; 0 means no promise was broken."""
+    dev = torch.device("cuda", torch.cuda.current_device() if device is None else
+                       (device if isinstance(device, int) else device.index or 0))
+    flags = _ffi.ctypes.c_int(0)
+    with torch.cuda.device(dev):
+        status = _ffi.lib().ss_attention_status(_ffi.ctypes.byref(flags), int(bool(clear)), _ffi.stream_ptr(dev))
+    _ffi.check(status, "attention_status")
+    return int(flags.value)
+
+
 def paged_attention_varlen(
     q: torch.Tensor,
     kv_cache: torch.Tensor,
@@ -291,6 +322,8 @@ def paged_attention_varlen(
     scale: float,
     block_size: int,
     max_query_len: int,
+    *,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Packed step: ``q`` ``[T, n_q, D]`` holds every sequence's new tokens back to back.
 
@@ -298,8 +331,12 @@ def paged_attention_varlen(
     ``context_lens[b]`` KV tokens (after this step's tokens were written), i.e.
     ``cu_seqlens = [0] + cumsum(query_lens)`` and ``context_lens = seq_lens`` of
     ``PagedForward`` (``slipstream/memory/paged_cache.py:35-54``).
-    ``max_query_len`` must bound every ``query_len`` (host-known, no sync).
-    Returns ``[T, n_q, D]``.
+    ``max_query_len`` must bound every ``query_len`` (host-known, no sync) and
+    ``cu_seqlens[-1] <= T``. A sequence longer than ``max_query_len`` gets zeros in its
+    uncovered rows and a stream past ``T`` is clamped; both set a bit that
+    :func:`attention_status` reports, and ``SLIPSTREAM_DEBUG`` raises ``ValueError`` for
+    them on the host before the launch. Returns ``[T, n_q, D]`` (written into ``out``
+    when given: same shape and dtype as ``q``, unit head_dim stride).
     """
     if q.ndim != 3:
         raise ValueError(f"q must be [T, n_q, D], got {tuple(q.shape)}")
@@ -315,7 +352,10 @@ def paged_attention_varlen(
         raise ValueError(f"block_tables must be [B={batch}, max_blocks], got {tuple(block_tables.shape)}")
     if max_query_len < 0:
         raise ValueError("max_query_len must be >= 0")
-    out = torch.empty((total, n_q, head_dim), device=q.device, dtype=q.dtype)
+    if out is None:
+        out = torch.empty((total, n_q, head_dim), device=q.device, dtype=q.dtype)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.device != q.device or out.stride(2) != 1:
+        raise ValueError(f"out must be {tuple(q.shape)} {q.dtype} on {q.device} with unit last stride")
     if batch == 0 or total == 0 or n_q == 0:
         return out
     require_device("paged_attention_varlen", q, kv_cache, block_tables, cu_seqlens, context_lens)
@@ -327,6 +367,8 @@ def paged_attention_varlen(
     block_tables = _int32(block_tables)
     cu = _int32(cu_seqlens.reshape(-1))
     ctx = _int32(context_lens.reshape(-1))
+    if _debug():
+        _check_stream(cu, total, max_query_len)
     kc = kv_cache[layer_idx, 0]
     vc = kv_cache[layer_idx, 1]
     if kc.stride(3) != 1 or kc.data_ptr() % 16 or vc.data_ptr() % 16:

@@ -8,6 +8,7 @@ packed description (``cu_seqlens`` / ``context_lens``) of one mixed step.
 
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass
 
 import torch
@@ -130,10 +131,19 @@ def build_packed_step(
     if block_tables.stride(1) != 1:
         block_tables = block_tables.contiguous()
     device = block_tables.device
-    # every entry is written by the kernel (no fill: the step may be graph-captured)
+    if os.environ.get("SLIPSTREAM_DEBUG", "0") not in {"0", "false", "False", ""} and batch:
+        ql = query_lens.cpu().clamp_min(0)
+        if int(ql.sum()) != total_tokens:
+            raise ValueError(f"total_tokens {total_tokens} != sum(query_lens) {int(ql.sum())}")
+        if int(ql.max()) > max_query_len:
+            raise ValueError(f"query_len {int(ql.max())} > max_query_len {max_query_len}")
+    # every entry is written by the kernel (no fill: the step may be graph-captured);
+    # slots past sum(query_lens) get -1, so a padded slot_mapping never scatters
     cu = torch.empty(batch + 1, dtype=torch.int32, device=device) if batch else torch.zeros(1, dtype=torch.int32)
     ctx = torch.empty(batch, dtype=torch.int32, device=device)
     slots = torch.empty(max(total_tokens, 0), dtype=torch.int64, device=device)
+    if not batch:
+        slots.fill_(-1)
     if batch:
         if device.type != "cuda":
             raise _ffi.KernelError(f"build_packed_step: slipstream_amd runs on HIP devices only; got {device}")

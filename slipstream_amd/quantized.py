@@ -38,7 +38,11 @@ def quantize_weight(weight: torch.Tensor, group_size: int) -> tuple[torch.Tensor
     zero_t = torch.zeros_like(w[..., :1])
     wmin = torch.minimum(w.amin(dim=-1, keepdim=True), zero_t)
     wmax = torch.maximum(w.amax(dim=-1, keepdim=True), zero_t)
-    scale = (wmax - wmin).clamp_min(1e-12) / _LEVELS
+    # A 0-d tensor divisor, not the Python number: on the GPU torch divides by a scalar
+    # as a multiplication by its reciprocal, which differs from the reference's
+    # (CPU) division in the last bit of about one scale in a few hundred.
+    levels = torch.full((), float(_LEVELS), dtype=w.dtype, device=w.device)
+    scale = (wmax - wmin).clamp_min(1e-12) / levels
     zero = torch.round(-wmin / scale).clamp_(0, _LEVELS)
     q = torch.clamp(torch.round(w / scale) + zero, 0, _LEVELS).reshape(out, k).to(torch.int64)
     shifts = torch.arange(0, 32, 4, device=weight.device, dtype=torch.int64)

@@ -24,7 +24,7 @@ def test_header_declares_entry_points():
     for required in ("ss_reshape_and_cache", "ss_paged_attention", "ss_paged_attention_varlen",
                      "ss_paged_attention_workspace_size", "ss_status_string", "ss_last_error",
                      "ss_w4a16_gemm", "ss_w4a16_workspace_size", "ss_copy_blocks", "ss_rope_and_cache",
-                     "ss_build_step_metadata", "ss_rmsnorm", "ss_swiglu"):
+                     "ss_build_step_metadata", "ss_rmsnorm", "ss_swiglu", "ss_attention_status"):
         assert required in names
 
 
@@ -196,3 +196,38 @@ def test_shared_prefix_argument_errors_need_no_device():
         paged_attention_shared_prefix(q, kv, bt, lens, 0, 0.1, 16, 9)
     with pytest.raises(RuntimeError, match="HIP devices only"):
         paged_attention_shared_prefix(q, kv, bt, lens, 0, 0.1, 16, 2)
+
+
+def test_attention_status_null_pointer_needs_no_device():
+    from slipstream_amd import _ffi
+
+    lib = _ffi.lib()
+    assert lib.ss_attention_status(None, 1, None) == _ffi.SS_ERR_INVALID
+    assert b"null" in lib.ss_last_error()
+
+
+def test_debug_checks_of_a_packed_step_run_on_the_host(monkeypatch):
+    """SLIPSTREAM_DEBUG: a slot count that is not the step's token count, or a query
+    longer than max_query_len, raises ValueError before any device work (the reference
+    raises for queries it cannot attend, attention.py:44-45)."""
+    import torch
+
+    from slipstream_amd.kernels.paged_attention import _check_stream
+    from slipstream_amd.paged_cache import build_packed_step
+
+    monkeypatch.setenv("SLIPSTREAM_DEBUG", "1")
+    bt = torch.zeros((2, 4), dtype=torch.int32)
+    prior = torch.tensor([3, 0], dtype=torch.int32)
+    ql = torch.tensor([1, 5], dtype=torch.int32)
+    with pytest.raises(ValueError, match="total_tokens"):
+        build_packed_step(bt, prior, ql, 16, 9, 5)
+    with pytest.raises(ValueError, match="max_query_len"):
+        build_packed_step(bt, prior, ql, 16, 6, 4)
+    cu = torch.tensor([0, 1, 6], dtype=torch.int32)
+    _check_stream(cu, 6, 5)
+    with pytest.raises(ValueError, match="max_query_len"):
+        _check_stream(cu, 6, 4)
+    with pytest.raises(ValueError, match="query tokens"):
+        _check_stream(cu, 5, 5)
+    with pytest.raises(ValueError, match="non-decreasing"):
+        _check_stream(torch.tensor([0, 4, 2], dtype=torch.int32), 6, 5)

@@ -19,7 +19,7 @@ from slipstream_amd.kernels import (
     paged_attention_varlen,
     reshape_and_cache,
 )
-from tests._helpers import assert_attn_close, bits, f64, gather_pool_f64, tables_array
+from tests._helpers import assert_attn_close, bits, f64, gather_pool_f64, oracle_paged_rows, tables_array
 
 pytestmark = pytest.mark.gpu
 
@@ -174,22 +174,48 @@ def test_decode_head_dim_64_and_256(device):
         assert_attn_close(out, ref, f"D={d}")
 
 
-def test_decode_full_llama_config_subset_checked(device):
+def test_decode_full_llama_config_every_row(device):
     """C2 at full size (256 sequences, lognormal lengths, 1.2x pool): the scatter of the
-    256 new tokens then split-K decode; 24 sequences (longest, shortest, random) checked."""
+    256 new tokens then split-K decode; every row against the float64 oracle."""
     b = workloads.llama_decode(device=device, seed=0)
     reshape_and_cache(b.k_new, b.v_new, b.kv_cache, b.slot_mapping, 0, 16)
     out = paged_attention_decode(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
     torch.cuda.synchronize()
-    ctx = np.array(b.ctx_host)
-    pick = sorted(set(np.argsort(ctx)[-8:].tolist() + np.argsort(ctx)[:8].tolist()
-                      + np.random.default_rng(0).choice(256, 8, replace=False).tolist()))
-    sub_tables = [b.tables_host[i] for i in pick]
-    pool, tables = gather_pool_f64(b.kv_cache, sub_tables)
-    q = f64(b.padded_q()[pick])
-    ref = ora.paged_attention(q, pool, tables_array(tables, max(len(t) for t in tables)), ctx[pick], 0,
-                              b.scale, 16)
-    assert_attn_close(out[pick], ref, "C2 subset")
+    q = f64(b.padded_q())
+    ref = oracle_paged_rows(b.kv_cache, b.tables_host, b.ctx_host, list(q), b.scale, 16)
+    assert_attn_close(out, np.stack(ref), "C2 every row")
+
+
+def test_decode_against_the_reference_dtype_path(device):
+    """Secondary check: the HIP decode against the reference's own dtype sequence
+    (oracle.reference_path: bf16/fp16 GEMMs, fp32 softmax, rounded to the dtype;
+    attention_ref.py:68-89, attention.py:64-88) at the C1 shape (fp16, 14/2 heads, D 64)
+    and on 16 Llama-3-8B-shape sequences (bf16). The distance is within the sum of the
+    two paths' bounds to the float64 oracle (HIP: 2e-3 + 1e-2|ref|; the reference's path:
+    its dtype's rounding, pinned in tests/test_oracle_reference_path.py); both distances
+    are recorded in the run's error summary."""
+    from oracle import reference_path as rp
+    from tests._helpers import record_error
+
+    for name, b, tol in (
+        ("C1 fp16", workloads.qwen05_decode(device="cpu", seed=0), (3e-3, 1.4e-2)),
+        ("Llama bf16", workloads.build_batch([17, 300, 1000, 2500, 64, 129, 511, 4096, 33, 800, 1500, 90, 16, 3000,
+                                               700, 250], [1] * 16, n_q=32, n_kv=8, head_dim=128, block_size=16,
+                                              dtype=torch.bfloat16, device="cpu", seed=4), (8e-3, 3e-2)),
+    ):
+        tables = torch.full((b.batch, b.block_tables.shape[1]), -1, dtype=torch.int32)
+        for i, t in enumerate(b.tables_host):
+            tables[i, : len(t)] = torch.tensor(t, dtype=torch.int32)
+        want = rp.paged_attention(b.padded_q(), b.kv_cache, tables, b.context_lens, 0, b.scale, b.block_size)
+        exact = _oracle_padded(b)
+        _to(b, device)
+        out = paged_attention_decode(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale,
+                                     b.block_size)
+        got = f64(out)
+        a, _ = record_error(f"{name}: HIP vs reference dtype path", got, f64(want))
+        record_error(f"{name}: reference dtype path vs float64", f64(want), exact)
+        assert_attn_close(out, exact, f"{name}: HIP vs float64")
+        np.testing.assert_allclose(got, f64(want), atol=tol[0], rtol=tol[1], err_msg=name)
 
 
 def test_decode_is_invariant_to_block_permutation(device):
@@ -420,24 +446,73 @@ def test_varlen_equals_padded_calls(device):
         assert_attn_close(out[cu[i]:cu[i + 1]], f64(oi[0]), f"sequence {i}")
 
 
-def test_varlen_full_mixed_step_subset_checked(device):
+def test_varlen_full_mixed_step_every_row(device):
     """C3 at full size: 192 decodes + 4 x 512-token chunks, 2240 tokens; the scatter then
-    attention; all decode rows of 12 sequences and the last 24 tokens of every chunk checked."""
+    attention; every row of every sequence against the float64 oracle."""
     b = workloads.mixed_step(device=device, seed=0)
     reshape_and_cache(b.k_new, b.v_new, b.kv_cache, b.slot_mapping, 0, 16)
     out = paged_attention_varlen(b.q, b.kv_cache, b.block_tables, b.cu_seqlens, b.context_lens, 0, b.scale,
                                  16, b.max_query_len)
     torch.cuda.synchronize()
     cu = b.cu_seqlens.cpu().tolist()
-    picks = list(range(0, 192, 16)) + list(range(192, 196))
-    pool, tables = gather_pool_f64(b.kv_cache, [b.tables_host[i] for i in picks])
-    for k, i in enumerate(picks):
+    q = f64(b.q)
+    queries = [q[cu[i]:cu[i + 1]].transpose(1, 0, 2) for i in range(b.batch)]
+    ref = oracle_paged_rows(b.kv_cache, b.tables_host, b.ctx_host, queries, b.scale, 16)
+    assert_attn_close(out, np.concatenate(ref, axis=0), "C3 every row")
+
+
+@pytest.mark.parametrize("max_q", [0, 1, 20, 40])
+def test_varlen_query_longer_than_max_query_len_is_zeroed_and_flagged(device, max_q):
+    """A packed sequence longer than max_query_len (a broken caller promise): the rows
+    no kernel of the call covers are written as zeros -- never left as stale memory --
+    and the device status word reports it; every covered row still matches the oracle.
+    max_q 0/1: no prefill launch (4 decode rows per KV head), so the 40- and 3-token
+    sequences are wholly zero; 20: the prefill covers 128 rows per KV head (tokens
+    0-31 of the 40-token chunk); 40: the promise holds, status stays 0."""
+    from slipstream_amd.kernels import attention_status
+
+    ctx, ql = [90, 500, 140, 60], [1, 1, 40, 3]
+    b = workloads.build_batch(ctx, ql, n_q=32, n_kv=8, head_dim=128, block_size=16, dtype=torch.bfloat16,
+                              device="cpu", seed=21)
+    ref = _oracle_varlen(b, f64(b.kv_cache))
+    _to(b, device)
+    attention_status(device)  # clear
+    out = torch.full_like(b.q, float("nan"))
+    paged_attention_varlen(b.q, b.kv_cache, b.block_tables, b.cu_seqlens, b.context_lens, 0, b.scale, 16,
+                           max_q, out=out)
+    flags = attention_status(device)
+    got = f64(out)
+    cu = [0, 1, 2, 42, 45]
+    covered_tokens = {0: [1, 1, 0, 0], 1: [1, 1, 0, 0], 20: [1, 1, 32, 3], 40: [1, 1, 40, 3]}[max_q]
+    for i in range(4):
         s0, s1 = cu[i], cu[i + 1]
-        m = min(24, s1 - s0)
-        qb = f64(b.q[s1 - m:s1]).transpose(1, 0, 2)
-        kk, vv, valid = ora.gather_kv(pool, 0, np.array(tables[k]), b.ctx_host[i], 16)
-        ref = ora.attend(qb, kk, vv, valid, b.ctx_host[i], b.scale)
-        assert_attn_close(out[s1 - m:s1], ref, f"C3 seq {i}")
+        c = s0 + covered_tokens[i]
+        if c > s0:
+            assert_attn_close(out[s0:c], ref[s0:c], f"covered rows of sequence {i}")
+        assert np.array_equal(got[c:s1], np.zeros_like(got[c:s1])), f"uncovered rows of sequence {i}"
+    assert flags == (0 if max_q == 40 else 1), flags
+    assert attention_status(device) == 0  # read-and-clear
+
+
+def test_varlen_stream_past_total_tokens_is_clamped_and_flagged(device):
+    """cu_seqlens running past the query tensor: every kernel clamps the sequences into
+    [0, T) (no read or write outside q and out), the earlier sequences are unaffected
+    and the status word reports the overrun."""
+    from slipstream_amd.kernels import attention_status
+
+    ctx, ql = [90, 500, 140, 60], [1, 1, 40, 3]
+    b = workloads.build_batch(ctx, ql, n_q=32, n_kv=8, head_dim=128, block_size=16, dtype=torch.bfloat16,
+                              device="cpu", seed=22)
+    ref = _oracle_varlen(b, f64(b.kv_cache))
+    _to(b, device)
+    attention_status(device)
+    q = b.q[:43].contiguous()  # the stream says 45 tokens
+    out = paged_attention_varlen(q, b.kv_cache, b.block_tables, b.cu_seqlens, b.context_lens, 0, b.scale, 16,
+                                 b.max_query_len)
+    flags = attention_status(device)
+    assert flags == 2, flags
+    assert_attn_close(out[:42], ref[:42], "sequences inside the stream")
+    assert np.isfinite(f64(out[42])).all()
 
 
 def test_varlen_packed_step_graph_replays(device):

@@ -16,7 +16,7 @@ import torch
 from oracle import paged_attention as ora
 from slipstream_amd import workloads
 from slipstream_amd.kernels import paged_attention_decode, paged_attention_shared_prefix
-from tests._helpers import assert_attn_close, f64, tables_array
+from tests._helpers import assert_attn_close, f64, oracle_paged_rows, tables_array
 
 pytestmark = pytest.mark.gpu
 
@@ -45,14 +45,28 @@ def test_c4_shape_reduced_batch(device):
 
 
 def test_c4_full_config(device):
-    """The full C4 batch (128 sequences): every row within tolerance of the plain decode,
-    a subset of rows against the oracle."""
+    """The full C4 batch (128 sequences): every row against the float64 oracle, and
+    within tolerance of the plain decode."""
     b = workloads.prefix_share(device=device, seed=0)
     out = _run(b, b.shared_blocks)
     plain = paged_attention_decode(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
+    torch.cuda.synchronize()
+    ref = np.stack(oracle_paged_rows(b.kv_cache, b.tables_host, b.ctx_host, list(f64(b.padded_q())), b.scale, 16))
+    assert_attn_close(out, ref, "C4 cascade every row")
+    assert_attn_close(plain, ref, "C4 plain decode every row")
     torch.testing.assert_close(out.float(), plain.float(), atol=2e-3, rtol=1e-2)
-    rows = [0, 1, 63, 127]
-    assert_attn_close(out[rows], _oracle(b, rows), "c4 subset")
+
+
+def test_prefix_is_the_whole_table(device):
+    """prefix_blocks == max_blocks: the suffix tables are empty (width 0), every sequence
+    is exactly the shared prefix, and the suffix part is empty (log-sum-exp -inf)."""
+    pb = 24
+    b = workloads.build_batch([pb * 16] * 40, [1] * 40, n_q=28, n_kv=4, head_dim=128, block_size=16,
+                              dtype=torch.bfloat16, device=device, seed=12, pool_factor=1.3,
+                              shared_prefix_blocks=pb)
+    assert b.block_tables.shape[1] == pb
+    out = _run(b, pb)
+    assert_attn_close(out, _oracle(b), "prefix == table")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

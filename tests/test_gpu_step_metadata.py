@@ -53,3 +53,34 @@ def test_device_metadata_equals_host_built_mixed_step(device):
     assert torch.equal(step.cu_seqlens, b.cu_seqlens.to(torch.int32))
     assert torch.equal(step.context_lens, b.context_lens.to(torch.int32))
     assert torch.equal(step.slot_mapping, b.slot_mapping)
+
+
+def test_slot_mapping_tail_past_the_step_is_minus_one(device):
+    """A slot_mapping longer than the step's tokens: the tail is -1 on the device (it was
+    stale memory, which the scatter would take for slots), through the C ABI on a buffer
+    pre-filled with in-pool slots, and through build_packed_step."""
+    from slipstream_amd import _ffi
+
+    tables = [[7, 9], [4], [11, 12, 13]]
+    prior, ql, bs, total = [3, 0, 20], [2, 5, 4], 16, 20
+    cu, ctx, want = ora.build_step_metadata(tables, prior, ql, bs, total_tokens=total)
+    assert want[11:].tolist() == [-1] * 9
+    bt = torch.full((3, 3), -1, dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, : len(t)] = torch.tensor(t, dtype=torch.int32)
+    bt = bt.to(device)
+    pr = torch.tensor(prior, dtype=torch.int32, device=device)
+    q = torch.tensor(ql, dtype=torch.int32, device=device)
+    cu_d = torch.empty(4, dtype=torch.int32, device=device)
+    ctx_d = torch.empty(3, dtype=torch.int32, device=device)
+    slots = torch.full((total,), 5, dtype=torch.int64, device=device)
+    st = _ffi.lib().ss_build_step_metadata(bt.data_ptr(), bt.stride(0), 3, pr.data_ptr(), q.data_ptr(), 3, bs,
+                                           cu_d.data_ptr(), ctx_d.data_ptr(), slots.data_ptr(), total,
+                                           _ffi.stream_ptr(device))
+    _ffi.check(st, "build_step_metadata")
+    torch.cuda.synchronize()
+    assert slots.cpu().numpy().tolist() == want.tolist()
+    assert cu_d.cpu().numpy().tolist() == cu.tolist() and ctx_d.cpu().numpy().tolist() == ctx.tolist()
+    step = build_packed_step(bt, pr, q, bs, total, 5)
+    torch.cuda.synchronize()
+    assert step.slot_mapping.cpu().numpy().tolist() == want.tolist()

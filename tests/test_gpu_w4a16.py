@@ -234,3 +234,28 @@ def test_c5_llama_layer_linears(device, k, n, name, m):
     zz = lin.qzeros[cols].cpu().numpy()
     ref = quant.w4a16_gemm(lin.x.double().cpu().numpy(), qw, sc, zz, lin.group_size)
     _assert_close(y[:, cols], ref, f"C5 {name} m={m} vs oracle")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("group", [32, 128])
+def test_device_quantizer_equals_oracle_quantizer(device, dtype, group):
+    """The load-time format producer (slipstream_amd.quantized.quantize_weight, a torch
+    restatement of quant_ref.py:72-100) run on the device: qweight and qzeros identical to
+    oracle.quant.quantize_w4a16 on the same weight, scales identical after the cast to the
+    weight's dtype (the reference returns them in weight.dtype). The weight has a constant
+    group (0 joins its range), an all-zero group and groups that hit both nibble ends."""
+    from slipstream_amd.quantized import quantize_weight
+
+    g = torch.Generator().manual_seed(group)
+    w = (torch.randn(96, 1024, generator=g) * 0.05).to(dtype)
+    w[3, :group] = 0.25
+    w[5, group : 2 * group] = 0.0
+    w[7, :group] = torch.linspace(-1.0, 1.0, group).to(dtype)
+    qw, s, z = quantize_weight(w.to(device), group)
+    rq, rs, rz = quant.quantize_w4a16(w.float().numpy(), group)
+    assert qw.dtype == torch.int32 and z.dtype == torch.int32 and s.dtype == dtype
+    assert np.array_equal(qw.cpu().numpy(), rq)
+    assert np.array_equal(z.cpu().numpy(), rz)
+    assert np.array_equal(s.cpu().float().numpy(), torch.from_numpy(rs).to(dtype).float().numpy())
+    u = quant.unpack_int4(rq, 1024)
+    assert u.min() == 0 and u.max() == 15

@@ -439,3 +439,12 @@ def test_step_metadata_edges():
     assert slots.tolist() == [3 * 8 + 6, 3 * 8 + 7, -1, -1]  # positions 8, 9 sit on the hole
     _, _, past = ora.build_step_metadata([[2]], [3], [3], 4)
     assert past.tolist() == [2 * 4 + 3, -1, -1]  # positions 4, 5 are past the one-block table
+
+
+def test_step_metadata_total_tokens_pads_and_cuts():
+    """An explicit slot count: entries past the step's tokens are -1 (no token owns them,
+    the scatter skips them), and a count below the step's tokens cuts the list."""
+    _, _, slots = ora.build_step_metadata([[3], [5]], [0, 2], [2, 1], 4, total_tokens=6)
+    assert slots.tolist() == [12, 13, 22, -1, -1, -1]
+    _, _, cut = ora.build_step_metadata([[3], [5]], [0, 2], [2, 1], 4, total_tokens=2)
+    assert cut.tolist() == [12, 13]
