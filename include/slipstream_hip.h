@@ -121,6 +121,28 @@ int ss_paged_attention_varlen(const void* q, void* out, const void* k_cache, con
                               int64_t workspace_bytes, void* stream);
 
 /*
+ * ss_paged_attention_varlen without a workspace argument: the decode split-K partials
+ * and the prefill work list live in a static device array of 64 MiB per GPU
+ * (allocated when the library's code object loads on that GPU, held until the
+ * process ends). No counterpart in the reference: it exists for callers that cannot
+ * allocate -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc. Same arguments, results and errors as ss_paged_attention_varlen
+ * (same kernels, bit-identical output); a call whose scratch need
+ * (ss_paged_attention_workspace_size) exceeds 64 MiB fails with SS_ERR_WORKSPACE
+ * before any device work. Allocates nothing. Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (two streams without ordering) race; order
+ * them on one stream. No part of the array must start at zero (every kernel writes
+ * what it later reads within the call).
+ */
+int ss_paged_attention_varlen_noalloc(const void* q, void* out, const void* k_cache, const void* v_cache,
+                                      const int32_t* block_tables, const int32_t* cu_seqlens,
+                                      const int32_t* context_lens, int64_t batch, int64_t total_tokens,
+                                      int n_q, int n_kv, int head_dim, int max_query_len, int max_blocks,
+                                      int block_size, int64_t num_blocks, const int64_t q_strides[2],
+                                      const int64_t o_strides[2], const int64_t c_strides[3],
+                                      int64_t bt_stride, float scale, int dtype, void* stream);
+
+/*
  * Device status word of the current GPU, OR-ed by the attention kernels when a
  * packed description breaks the caller's promises (SS_STATUS_* bits):
  *   SS_STATUS_QUERY_TOO_LONG  a sequence of ss_paged_attention_varlen had more query

@@ -66,6 +66,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _c_i64p, _c_i64p, _c_i64p, _i64, ctypes.c_float, _i32, _vp, _i64, _vp,
         ],
     ),
+    "ss_paged_attention_varlen_noalloc": (
+        _i32,
+        [
+            _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i64,
+            _c_i64p, _c_i64p, _c_i64p, _i64, ctypes.c_float, _i32, _vp,
+        ],
+    ),
     "ss_w4a16_workspace_size": (_i32, [_i64, _i64, _i64, _i32, _i32, _c_i64p]),
     "ss_w4a16_gemm": (
         _i32,

@@ -2,6 +2,7 @@
 // decode kernel for sequences whose query rows fit one 16-row MFMA tile, and
 // the prefill kernel for the rest.
 #include <algorithm>
+#include <mutex>
 
 #include "attention_common.h"
 
@@ -183,15 +184,14 @@ extern "C" int ss_paged_attention(const void* q, void* out, const void* k_cache,
   return run(p, dtype, head_dim, tq, workspace, workspace_bytes, (hipStream_t)stream, decode, !decode);
 }
 
-extern "C" int ss_paged_attention_varlen(const void* q, void* out, const void* k_cache, const void* v_cache,
-                                         const int32_t* block_tables, const int32_t* cu_seqlens,
-                                         const int32_t* context_lens, int64_t batch, int64_t total_tokens,
-                                         int n_q, int n_kv, int head_dim, int max_query_len, int max_blocks,
-                                         int block_size, int64_t num_blocks, const int64_t q_strides[2],
-                                         const int64_t o_strides[2], const int64_t c_strides[3],
-                                         int64_t bt_stride, float scale, int dtype, void* workspace,
-                                         int64_t workspace_bytes, void* stream) {
-  const char* who = "paged attention varlen";
+namespace {
+
+int varlen_impl(const char* who, const void* q, void* out, const void* k_cache, const void* v_cache,
+                const int32_t* block_tables, const int32_t* cu_seqlens, const int32_t* context_lens, int64_t batch,
+                int64_t total_tokens, int n_q, int n_kv, int head_dim, int max_query_len, int max_blocks,
+                int block_size, int64_t num_blocks, const int64_t q_strides[2], const int64_t o_strides[2],
+                const int64_t c_strides[3], int64_t bt_stride, float scale, int dtype, void* workspace,
+                int64_t workspace_bytes, void* stream) {
   int st = check_common(who, n_q, n_kv, head_dim, block_size, dtype, max_blocks, num_blocks);
   if (st != SS_OK) return st;
   if (batch < 0 || total_tokens < 0 || max_query_len < 0) {
@@ -232,6 +232,80 @@ extern "C" int ss_paged_attention_varlen(const void* q, void* out, const void* k
   const bool prefill = (int64_t)max_query_len * p.n_rep > ss::kDecodeRows;
   return run(p, dtype, head_dim, max_query_len, workspace, workspace_bytes, (hipStream_t)stream, true,
              prefill);
+}
+
+// Scratch of the no-alloc entry point: one array per GPU, held until the process
+// ends. Host code never uses its name as an address (on the host it is a stand-in
+// symbol); scratch_ptr() resolves this device's copy with hipGetSymbolAddress once
+// per device, and only that pointer reaches the kernels.
+constexpr int64_t kScratchBytes = 64ll << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[64] = {nullptr};
+
+void* scratch_ptr(const char* who) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    ss_host::set_error("%s: no current HIP device", who);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr) {
+      ss_host::set_error("%s: hipGetSymbolAddress of the scratch array failed on device %d: %s", who, dev,
+                         hipGetErrorString(err));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int ss_paged_attention_varlen(const void* q, void* out, const void* k_cache, const void* v_cache,
+                                         const int32_t* block_tables, const int32_t* cu_seqlens,
+                                         const int32_t* context_lens, int64_t batch, int64_t total_tokens,
+                                         int n_q, int n_kv, int head_dim, int max_query_len, int max_blocks,
+                                         int block_size, int64_t num_blocks, const int64_t q_strides[2],
+                                         const int64_t o_strides[2], const int64_t c_strides[3],
+                                         int64_t bt_stride, float scale, int dtype, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+  return varlen_impl("paged attention varlen", q, out, k_cache, v_cache, block_tables, cu_seqlens, context_lens,
+                     batch, total_tokens, n_q, n_kv, head_dim, max_query_len, max_blocks, block_size, num_blocks,
+                     q_strides, o_strides, c_strides, bt_stride, scale, dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ss_paged_attention_varlen_noalloc(const void* q, void* out, const void* k_cache, const void* v_cache,
+                                                 const int32_t* block_tables, const int32_t* cu_seqlens,
+                                                 const int32_t* context_lens, int64_t batch, int64_t total_tokens,
+                                                 int n_q, int n_kv, int head_dim, int max_query_len, int max_blocks,
+                                                 int block_size, int64_t num_blocks, const int64_t q_strides[2],
+                                                 const int64_t o_strides[2], const int64_t c_strides[3],
+                                                 int64_t bt_stride, float scale, int dtype, void* stream) {
+  const char* who = "paged attention varlen (no-alloc)";
+  // nothing to attend, or an argument error: the shared body returns without the scratch
+  if (batch <= 0 || total_tokens <= 0 || n_q < 1 || n_kv < 1 || n_q % n_kv != 0)
+    return varlen_impl(who, q, out, k_cache, v_cache, block_tables, cu_seqlens, context_lens, batch, total_tokens,
+                       n_q, n_kv, head_dim, max_query_len, max_blocks, block_size, num_blocks, q_strides, o_strides,
+                       c_strides, bt_stride, scale, dtype, nullptr, 0, stream);
+  int64_t need = 0;
+  int st = ss_paged_attention_workspace_size(batch, n_q, n_kv, head_dim, max_query_len < 1 ? 1 : max_query_len,
+                                             dtype, &need);
+  if (st != SS_OK) return st;
+  if (need > kScratchBytes) {
+    ss_host::set_error("%s: needs %lld bytes of scratch (batch %lld, max_query_len %d), the static scratch holds "
+                       "%lld; use ss_paged_attention_varlen with a workspace", who, (long long)need,
+                       (long long)batch, max_query_len, (long long)kScratchBytes);
+    return SS_ERR_WORKSPACE;
+  }
+  void* ws = scratch_ptr(who);
+  if (!ws) return SS_ERR_LAUNCH;
+  return varlen_impl(who, q, out, k_cache, v_cache, block_tables, cu_seqlens, context_lens, batch, total_tokens,
+                     n_q, n_kv, head_dim, max_query_len, max_blocks, block_size, num_blocks, q_strides, o_strides,
+                     c_strides, bt_stride, scale, dtype, ws, kScratchBytes, stream);
 }
 
 // ---- shared-prefix cascade -------------------------------------------------
