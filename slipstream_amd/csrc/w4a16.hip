@@ -22,8 +22,10 @@
 // while the current one computes), and one LDS pass adds the slices in wave
 // order. There is no synchronisation between workgroups.
 //
-// Tiled kernel (w4a16_tile_kernel, m >= 2 and g % 128 == 0; m <= 16 only for
-// K >= 8192 or N >= 24576): four waves split 64*NS weight rows and share the activation tile
+// Skinny kernel (w4a16_skinny_kernel, 2 <= m <= 16 and g == 128): the waves of one
+// workgroup split K for 16*NS weight rows, activations staged per wave through LDS,
+// no partials leave the workgroup. Tiled kernel (w4a16_tile_kernel, m > 16 and
+// g % 128 == 0): four waves split 64*NS weight rows and share the activation tile
 // through LDS; K is split over workgroups and a second kernel adds the fp32
 // partials in range order. Batch 1 takes a bandwidth GEMV. In every case the
 // result does not depend on timing.
@@ -669,6 +671,184 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
+// Skinny kernel (2 <= m <= 16, g == 128): bandwidth-bound shapes without a K split
+// across workgroups. A workgroup owns 16*NS weight rows and KW waves; wave w takes the
+// 128*ST keys [w*128*ST, (w+1)*128*ST) of those rows and of the 16*MT activation rows,
+// P stages of 128 keys in flight (weights non-temporal). Per stage and weight tile: four
+// MFMAs G = sum x (MAGIC + q), and per activation tile four MFMAs X = sum x against an
+// all-ones operand; the fold acc += s G - s (MAGIC + z) X is exact for any zero point.
+// The waves' partial sums meet in LDS and are added in wave order (deterministic).
+//   - A stage is one quantisation group (g == 128), so a lane needs the scale and zero
+//     point of its own weight row for ST consecutive groups: one load each for all its
+//     stages, issued before the stream (scattered per-stage scale loads took the
+//     address unit's cycles from the weight stream).
+//   - Activations: instruction s of a stage reads rows 4 s .. 4 s + 3 of the tile, 256
+//     contiguous bytes each (whole cache lines; the MFMA layout read directly from memory
+//     -- 16 rows x 64 bytes per instruction at the rows' stride -- measured about twice as
+//     slow on the activation side), and the wave writes the stage to its own LDS buffer
+//     and reads it back in the MFMA A layout (rows padded by 16 bytes: no bank conflicts).
+//     The buffer is private to the wave, whose LDS operations run in order: no barrier.
+template <typename T, int MT, int NS>
+struct SkinnyStage {
+  u32x4 xa[MT][4];  // activation rows 4 s + kg of the tile, keys 8 (lane & 15) .. + 7 of the stage
+  u32x4 w[NS];      // 32 nibbles: row 16 ns + (lane & 15), keys 32 kg .. + 31
+};
+constexpr int kSkinnyXRow = 256 + 16;  // LDS bytes of one staged activation row (128 keys + pad)
+
+template <typename T, int MT, int NS, int ST, int P, int LB>
+__global__ __launch_bounds__(LB) void w4a16_skinny_kernel(const W4Params p) {
+  typedef W4Elem<T> E;
+  typedef SkinnyStage<T, MT, NS> Stage;
+  extern __shared__ __attribute__((aligned(16))) char s_dyn[];
+  constexpr int NE = MT * NS * 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kw = blockDim.x >> 6;
+  float* const s_red = (float*)s_dyn;  // [KW][MT * NS * 4][64]
+  char* const s_xw = s_dyn + (size_t)kw * NE * 64 * 4 + (size_t)wave * MT * 16 * kSkinnyXRow;  // this wave's
+  const int ln = lane & 15, kg = lane >> 4;
+  const int n0 = blockIdx.x * 16 * NS;
+  const int m0 = blockIdx.y * 16 * MT;
+  const int rows = min(16 * MT, p.m - m0);
+  const int k0 = wave * 128 * ST;
+  const uint32_t magic = in_vgpr(E::kMagicPair);
+
+  // scale and zero point of this lane's rows for the wave's ST groups (g == 128): ST
+  // scales of esize bytes and ST int32 zero points, contiguous in each row
+  const int esize = p.sdt == SS_DTYPE_F32 ? 4 : 2;
+  const uint32_t f16_mask = p.sdt == SS_DTYPE_F16 ? ~0u : 0u, bf16_mask = p.sdt == SS_DTYPE_BF16 ? ~0u : 0u;
+  const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.sc, (uint32_t)((int64_t)p.n * p.groups * esize));
+  const __amdgpu_buffer_rsrc_t rzp = buffer_rsrc(p.qz, (uint32_t)((int64_t)p.n * p.groups * 4));
+  // ST fp32 scales, or ST 16-bit scales from the dword holding the first (ST / 2 + 1
+  // dwords cover them whether that one starts at a low or a high half)
+  uint32_t sdw[NS][ST + 1];
+  int zv[NS][ST];
+  const int nsd = esize == 4 ? ST : ST / 2 + 1;
+#pragma unroll
+  for (int ns = 0; ns < NS; ++ns) {
+    const int gi = min(n0 + 16 * ns + ln, p.n - 1) * p.groups + k0 / 128;
+#pragma unroll
+    for (int d = 0; d <= ST; ++d)
+      sdw[ns][d] =
+          d < nsd ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsc, (gi * esize & ~3) + 4 * d, 0, 0) : 0u;
+#pragma unroll
+    for (int i = 0; i < ST; ++i) zv[ns][i] = __builtin_amdgcn_raw_buffer_load_b32(rzp, (gi + i) * 4, 0, 0);
+  }
+  // scale of stage i, tile ns: 16-bit scales start at the low half when gi is even
+  auto stage_scale = [&](int ns, int i) {
+    const int gi0 = min(n0 + 16 * ns + ln, p.n - 1) * p.groups + k0 / 128;
+    uint32_t bits;
+    if (esize == 4) {
+      bits = sdw[ns][i];
+    } else {
+      const int h = (gi0 & 1) + i;  // 16-bit index from the first loaded dword
+      bits = sdw[ns][h >> 1] >> (16 * (h & 1));
+    }
+    return decode_scale_masked(bits, f16_mask, bf16_mask);
+  };
+
+  // activation rows [m0, m0 + rows): a row past them reads as zero (its byte offset is at
+  // least rows * x_stride * sizeof(T), past the descriptor's end as x_stride >= K)
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(
+      (const T*)p.x + (int64_t)m0 * p.x_stride, (uint32_t)(((int64_t)(rows - 1) * p.x_stride + p.k) * sizeof(T)));
+  int x_off[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      x_off[mt][s] = (int)(((int64_t)(16 * mt + 4 * s + kg) * p.x_stride + k0 + 8 * ln) * (int64_t)sizeof(T));
+  // weight rows [n0, n0 + 16 NS) that exist; rows past N read as zero and are never stored
+  const int live = min(16 * NS, p.n - n0);
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(p.qw + (int64_t)n0 * (p.k / 8), (uint32_t)live * (uint32_t)(p.k / 2));
+  int w_off[NS];
+#pragma unroll
+  for (int ns = 0; ns < NS; ++ns) w_off[ns] = (16 * ns + ln) * (p.k / 2) + k0 / 2 + 16 * kg;
+
+  auto issue = [&](int i, Stage& st) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        st.xa[mt][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, x_off[mt][s], 256 * i, 0));
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns)
+      st.w[ns] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, w_off[ns], 64 * i, kNonTemporal));
+  };
+
+  f32x4 acc[MT][NS];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) acc[mt][ns] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  const uint32_t one2 = in_vgpr(E::kOnePair);
+  const u32x4 ones = {one2, one2, one2, one2};
+
+  auto compute = [&](Stage& st, int i) {
+    u32x4 a[MT][4];
+    f32x4 X[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      char* const tile = s_xw + mt * 16 * kSkinnyXRow;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) store16(tile + (4 * s + kg) * kSkinnyXRow + 16 * ln, st.xa[mt][s]);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) a[mt][s] = permute_x(load16(tile + ln * kSkinnyXRow + 64 * kg + 16 * s));
+      X[mt] = Elem<T>::mfma(a[mt][0], ones, zero4);
+#pragma unroll
+      for (int s = 1; s < 4; ++s) X[mt] = Elem<T>::mfma(a[mt][s], ones, X[mt]);
+    }
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) {
+      f32x4 G[MT];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const u32x4 b = nibbles_to_operand(st.w[ns][s], magic);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) G[mt] = Elem<T>::mfma(a[mt][s], b, s == 0 ? zero4 : G[mt]);
+      }
+      const float sc = stage_scale(ns, i);
+      const float szm = sc * (E::kMagic + (float)zv[ns][i]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[mt][ns][e] = fmaf(sc, G[mt][e], fmaf(-szm, X[mt][e], acc[mt][ns][e]));
+    }
+  };
+
+  Stage ring[P];
+#pragma unroll
+  for (int u = 0; u < P; ++u) issue(u, ring[u]);
+#pragma unroll
+  for (int i = 0; i < ST; ++i) {
+    compute(ring[i % P], i);
+    if (i + P < ST) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue(i + P, ring[i % P]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // the waves' K slices, added in wave order
+  float* mine = s_red + (size_t)wave * NE * 64;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mine[((mt * NS + ns) * 4 + e) * 64 + lane] = acc[mt][ns][e];
+  __syncthreads();
+  for (int t = threadIdx.x; t < NE * 64; t += blockDim.x) {
+    float y = 0.f;
+    for (int w2 = 0; w2 < kw; ++w2) y += s_red[(size_t)w2 * NE * 64 + t];
+    const int idx = t >> 6, l = t & 63;
+    const int e = idx & 3, ns = (idx >> 2) % NS, mt = (idx >> 2) / NS;
+    const int m = m0 + 16 * mt + 4 * (l >> 4) + e;
+    const int n = n0 + 16 * ns + (l & 15);
+    if (m < p.m && n < p.n) ((T*)p.out)[(int64_t)m * p.o_stride + n] = (T)y;
+  }
+}
+
 // out[m][n] = sum over ranges z (in order) of part[z][m][n]; VEC consecutive n per thread.
 template <typename T, int VEC>
 __global__ __launch_bounds__(256) void w4a16_splitk_reduce_kernel(const float* __restrict__ part, void* out, int m,
@@ -887,6 +1067,8 @@ struct W4Plan {
   bool xlds;
   int gemv;  // 1: the batch-1 GEMV kernel
   bool tile;  // the tiled kernel (activations shared through LDS)
+  bool skinny;  // the skinny kernel (m <= 64, K split over the waves of one workgroup)
+  int st;       // skinny: 128-key stages per wave
   int mt, ns, bit, kw, pf;
   int m_blocks, n_tiles;
   int ks, kchunk;  // tiled kernel: K ranges and 128-key stages per range
@@ -954,6 +1136,53 @@ bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
   return true;
 }
 
+// Skinny kernel for 1 <= m <= 64 with g % 128 == 0: the K split stays inside one
+// workgroup (K = KW waves x 128 ST keys, KW <= 16), so no partials leave it. Activation
+// tiles MT = ceil(m / 16) (at most 4); NS = 2 weight tiles per wave when that still
+// leaves >= 2048 waves (halves the activation reads), else 1.
+constexpr size_t kSkinnyLdsMax = 128 * 1024;
+
+bool plan_skinny(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
+  if (!pl.wide || m < 2 || m > 16 || g != 128) return false;
+  const int64_t q = k / 128;
+  int st = 0;
+  for (int c : {4, 8, 2, 1})
+    if (q % c == 0 && q / c <= 16) {
+      st = c;
+      break;
+    }
+  if (!st) return false;
+  const int mt = 1;
+  int kw = (int)(q / st);
+  const int64_t m_blocks = (m + 16 * mt - 1) / (16 * mt);
+  // four weight tiles per wave: each activation fragment serves 64 weight rows, so the
+  // activation reads (L2) match the weight bytes; needs the 256 registers of a
+  // workgroup of at most 8 waves (ST 4 or 8)
+  // the fewest weight tiles per wave that keep the grid within one workgroup per CU:
+  // every workgroup stages all of its activation rows' K, so fewer, wider workgroups
+  // read fewer activation bytes (four tiles need at most 8 waves and 4 or 8 stages)
+  const int64_t cus = ss_host::device_cu_count();
+  int ns = 4;
+  for (int c : {1, 2})
+    if ((n + 16 * c - 1) / (16 * c) * m_blocks <= cus) {
+      ns = c;
+      break;
+    }
+  if (ns == 4 && (kw > 8 || st != 4)) ns = 2;  // four tiles: 256 registers (<= 8 waves), 4 stages
+  if (ns == 2 && st > 4) ns = 1;                 // two tiles of 8 stages exceed 128 registers
+  const size_t lds = (size_t)kw * mt * ns * 4 * 64 * 4 + (size_t)kw * mt * 16 * kSkinnyXRow;
+  if (lds > kSkinnyLdsMax) return false;
+  const int64_t n_tiles = (n + 16 * ns - 1) / (16 * ns);
+  if (n_tiles > 0x7fffffff) return false;
+  // activation fragments are addressed by 32-bit byte offsets within a 16*MT-row block
+  pl.skinny = true;
+  pl.mt = mt, pl.ns = ns, pl.st = st, pl.kw = kw;
+  pl.n_tiles = (int)n_tiles;
+  pl.m_blocks = (int)m_blocks;
+  pl.lds = lds;
+  return true;
+}
+
 int64_t tile_workspace_bytes(const W4Plan& pl, int64_t m, int64_t n) {
   return pl.tile && pl.ks > 1 ? (int64_t)pl.ks * m * n * 4 : 0;
 }
@@ -980,6 +1209,7 @@ W4Plan plan_w4a16(int64_t m, int64_t n, int64_t k, int g, bool act16, bool allow
       return pl;
     }
   }
+  if (plan_skinny(pl, m, n, k, g)) return pl;
   if (allow_tile && plan_tile(pl, m, n, k, g)) return pl;
   pl.tile = false;
   const size_t unit = pl.wide ? 128 : 32;
@@ -1058,8 +1288,65 @@ int launch_w4a16_tile(const W4Params& p, const W4Plan& pl, float* part, hipStrea
   return ss_host::launch_status("w4a16 split-K reduce");
 }
 
+template <typename T, int MT, int NS, int ST>
+int launch_w4a16_skinny_st(const W4Params& p, const W4Plan& pl, hipStream_t stream) {
+  // stages in flight: four, or two where four would not fit the registers (eight stages
+  // of four weight tiles; eight stages under the 128 registers of 16-wave workgroups)
+  constexpr int P4 = 4 < ST ? 4 : ST;
+  constexpr int P2 = 2 < ST ? 2 : ST;
+  // 16-wave workgroups get 128 registers a lane; up to 8 waves, 256
+  auto launch = [&](auto kern) {
+    static bool attr_set = false;  // per instantiation; the attribute is process-wide
+    if (!attr_set) {
+      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSkinnyLdsMax) !=
+          hipSuccess) {
+        ss_host::set_error("w4a16 gemm: cannot reserve %d bytes of LDS", (int)kSkinnyLdsMax);
+        return SS_ERR_UNSUPPORTED;
+      }
+      attr_set = true;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)pl.n_tiles, (unsigned)pl.m_blocks), dim3((unsigned)(64 * pl.kw)), pl.lds,
+                       stream, p);
+    return ss_host::launch_status("w4a16 gemm (skinny)");
+  };
+  if (pl.kw > 8) {
+    if constexpr (NS <= 2) return launch(w4a16_skinny_kernel<T, MT, NS, ST, ST >= 8 ? P2 : P4, 1024>);
+    ss_host::set_error("w4a16 gemm: skinny plan with %d waves and %d weight tiles", pl.kw, NS);
+    return SS_ERR_UNSUPPORTED;
+  }
+  return launch(w4a16_skinny_kernel<T, MT, NS, ST, NS >= 4 && ST >= 8 ? P2 : P4, 512>);
+}
+
+template <typename T, int MT>
+int launch_w4a16_skinny_mt(const W4Params& p, const W4Plan& pl, hipStream_t stream) {
+  if (pl.ns == 4) {
+    if (pl.st == 4) return launch_w4a16_skinny_st<T, MT, 4, 4>(p, pl, stream);
+    ss_host::set_error("w4a16 gemm: skinny plan with 4 weight tiles and %d stages", pl.st);
+    return SS_ERR_UNSUPPORTED;
+  }
+  if (pl.ns == 2) {
+    switch (pl.st) {
+      case 1: return launch_w4a16_skinny_st<T, MT, 2, 1>(p, pl, stream);
+      case 2: return launch_w4a16_skinny_st<T, MT, 2, 2>(p, pl, stream);
+      case 4: return launch_w4a16_skinny_st<T, MT, 2, 4>(p, pl, stream);
+      default: break;
+    }
+  } else {
+    switch (pl.st) {
+      case 1: return launch_w4a16_skinny_st<T, MT, 1, 1>(p, pl, stream);
+      case 2: return launch_w4a16_skinny_st<T, MT, 1, 2>(p, pl, stream);
+      case 4: return launch_w4a16_skinny_st<T, MT, 1, 4>(p, pl, stream);
+      case 8: return launch_w4a16_skinny_st<T, MT, 1, 8>(p, pl, stream);
+      default: break;
+    }
+  }
+  ss_host::set_error("w4a16 gemm: skinny plan with %d weight tiles and %d stages", pl.ns, pl.st);
+  return SS_ERR_UNSUPPORTED;
+}
+
 template <typename T>
 int launch_w4a16_typed(const W4Params& p, const W4Plan& pl, float* part, hipStream_t stream) {
+  if (pl.skinny) return launch_w4a16_skinny_mt<T, 1>(p, pl, stream);
   if (pl.tile) {
     if (pl.mt == 1) return launch_w4a16_tile<T, 1, 2, 8>(p, pl, part, stream);
     if (pl.mt == 2) return launch_w4a16_tile<T, 2, 2, 8>(p, pl, part, stream);
