@@ -594,9 +594,9 @@ extern "C" int ss_paged_attention_shared_prefix(const void* q, void* out, const 
     ps.ctx_lens = sctx;
     ps.lse = lse + (int64_t)pl.S * rows;
     ps.rmax = ss::decode_rows_for(1, ps.n_rep);
-    // suffixes are short (C4: about nine 32-key pairs each): one range per CU splits
-    // fewer of them across workgroups than the occupancy's two (measured 47.6 against
-    // 51.1 us at C4; 192 and 128 ranges were slower)
+    // suffixes are short (C4: about nine 32-key pairs each): one range per CU and head
+    // group at most (measured 47.6 us at C4 against 51.1 us for two; 192 and 128 ranges
+    // were slower)
     ps.range_cap = ss_host::device_cu_count();
     st = ss::launch_decode(ps, dtype, head_dim, 1, ws, pl.dec, s);
     if (st != SS_OK) return st;
