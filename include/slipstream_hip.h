@@ -148,7 +148,10 @@ int ss_paged_attention_varlen_noalloc(const void* q, void* out, const void* k_ca
  *   SS_STATUS_QUERY_TOO_LONG  a sequence of ss_paged_attention_varlen had more query
  *     tokens than max_query_len covers; its uncovered rows were written as zeros;
  *   SS_STATUS_STREAM_OVERRUN  cu_seqlens ran past total_tokens (or backwards); the
- *     kernels clamped every sequence into [0, total_tokens).
+ *     kernels clamped every sequence into [0, total_tokens);
+ *   SS_STATUS_PREFIX_SHORT  a sequence of ss_paged_attention_shared_prefix had fewer
+ *     KV tokens than the shared prefix; its suffix counted as empty (it attended the
+ *     whole prefix).
  * The reference raises ValueError at such inputs (slipstream/models/layers/attention.py:44-45);
  * a device kernel cannot, so it writes defined values and reports here. Waits for
  * `stream`, then stores the word in *flags and clears it when `clear` is nonzero.
@@ -156,6 +159,7 @@ int ss_paged_attention_varlen_noalloc(const void* q, void* out, const void* k_ca
  */
 #define SS_STATUS_QUERY_TOO_LONG 1
 #define SS_STATUS_STREAM_OVERRUN 2
+#define SS_STATUS_PREFIX_SHORT 4
 int ss_attention_status(int* flags, int clear, void* stream);
 
 /*
@@ -166,16 +170,19 @@ int ss_attention_status(int* flags, int clear, void* stream);
  * (slipstream/kernels/paged_attention.py:21-40, ss_paged_attention with tq = 1) up to
  * rounding, but the shared prefix is read once for the whole batch: its chunks are
  * attended by every sequence's query rows together, the private suffixes by the
- * decode, and the parts merged by log-sum-exp weights.
- * Caller's promise: block_tables(b, i) == block_tables(0, i) for i < prefix_blocks and
- * seq_lens[b] >= prefix_blocks * block_size for every b (not checked on the device).
+ * decode, and the parts merged by log-sum-exp weights (two kernel launches plus the
+ * decode's merge).
+ * Caller's promise: block_tables(b, i) == block_tables(0, i) for i < prefix_blocks
+ * (not checked on the device; the prefix pass reads the first row) and
+ * seq_lens[b] >= prefix_blocks * block_size for every b (a shorter sequence raises
+ * SS_STATUS_PREFIX_SHORT, see ss_attention_status).
  * Batches with batch * n_q / n_kv <= 16, n_q / n_kv > 16, head_dim 256 or blocks of
  * fewer than 16 tokens run the plain decode path instead.
  * q(b, h, d) = q + b*q_strides[0] + h*q_strides[1] + d; out likewise with o_strides.
  * workspace: at least ss_paged_attention_shared_prefix_workspace_size() bytes (the
- * decode partials, the prefix pass's work list, chunk metadata, the parts' log-sum-exp
- * and the prefix parts: S * batch * n_q * head_dim elements, S ~ CU count / (query
- * tiles * n_kv)).
+ * decode partials, the prefix parts and their log-sum-exp: S * batch * n_q * head_dim
+ * elements, S ~ CU count / (query tiles * n_kv), and fp32 rows of the suffixes:
+ * batch * n_q * (head_dim + 2) floats).
  */
 int ss_paged_attention_shared_prefix_workspace_size(int64_t batch, int n_q, int n_kv, int head_dim,
                                                     int block_size, int prefix_blocks, int dtype,

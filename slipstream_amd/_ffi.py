@@ -24,6 +24,7 @@ SS_ERR_WORKSPACE = 4
 
 SS_STATUS_QUERY_TOO_LONG = 1
 SS_STATUS_STREAM_OVERRUN = 2
+SS_STATUS_PREFIX_SHORT = 4
 
 SS_DTYPE_F16 = 0
 SS_DTYPE_BF16 = 1

@@ -48,12 +48,25 @@ struct AttnParams {
   // sequence (a query longer than the call's max_query_len) are written as zeros
   // by the decode merge, which also raises kStatusQueryTooLong.
   int row_cap;
+  // Shared-prefix cascade (zero / nullptr otherwise):
+  int ctx_shift;      // KV length of sequence b = ctx_lens[b] - ctx_shift (at least 0)
+  int chunk_tokens;   // > 0: sequence b is chunk b of a prefix of prefix_tokens keys:
+  int prefix_tokens;  //   min(chunk_tokens, prefix_tokens - b * chunk_tokens) keys, no
+                      //   ctx_lens, and query tokens [b * q_period, (b + 1) * q_period)
+  int work_qtiles;    // > 0: the prefill takes entry e = (e / work_qtiles, e % work_qtiles)
+                      //   of batch * work_qtiles, in order, instead of a work list
+  const void* px_part;  // S normalised prefix parts [S][batch * n_q][D] of the head_dim type
+  const float* px_lse;  // and their log2-domain log-sum-exp [S][batch * n_q]
+  int px_n;             // S: the decode and its merge fold the parts into every row
+  float* px_seq_o;      // fp32 (acc, then max and sum) of the rows of sequences the decode
+  float* px_seq_ml;     //   finishes inside one range: [batch * n_q][D], [batch * n_q][2]
 };
 
 // Bits of the device status word (ss_attention_status): set by kernels that met a
 // packed description they could not compute, never cleared by them.
 constexpr int kStatusQueryTooLong = 1;   // qlen > max_query_len: rows zero-filled
 constexpr int kStatusStreamOverrun = 2;  // cu_seqlens beyond total_tokens: clamped
+constexpr int kStatusPrefixShort = 4;    // shared prefix longer than a sequence's seq_len
 
 // Decode tile: one wave covers up to 16 query rows (query token j, head i in
 // the GQA group) of one KV head; r = j * n_rep + i.
@@ -62,7 +75,10 @@ constexpr int kDecodeRows = 16;
 constexpr int kPairTokens = 32;
 
 __device__ __forceinline__ void seq_queries(const AttnParams& p, int b, int& qlen, int64_t& qoff) {
-  if (p.cu) {
+  if (p.chunk_tokens > 0) {
+    qlen = p.q_period;
+    qoff = (int64_t)b * p.q_period;
+  } else if (p.cu) {
     const int s = min(max(p.cu[b], 0), p.total_tokens);
     const int e = min(max(p.cu[b + 1], s), p.total_tokens);
     qlen = e - s;
@@ -73,10 +89,18 @@ __device__ __forceinline__ void seq_queries(const AttnParams& p, int b, int& qle
   }
 }
 
-// Index of a query row's log-sum-exp: packed token (or b * tq + t) times n_q, plus head.
+// Index of a query row's log-sum-exp: packed (or prefix-chunk) token, else b * tq + t,
+// times n_q, plus head.
 __device__ __forceinline__ int64_t lse_index(const AttnParams& p, int b, int64_t qoff, int j, int hq) {
-  const int64_t tok = p.cu ? qoff + j : (int64_t)b * p.tq + j;
+  const int64_t tok = (p.cu || p.chunk_tokens > 0) ? qoff + j : (int64_t)b * p.tq + j;
   return tok * p.n_q + hq;
+}
+
+// KV length of sequence b (context_lens / seq_lens, negative counts as 0).
+__device__ __forceinline__ int kv_len(const AttnParams& p, int b) {
+  if (p.chunk_tokens > 0) return min(p.chunk_tokens, p.prefix_tokens - b * p.chunk_tokens);
+  const int c = p.ctx_lens[b] - p.ctx_shift;
+  return c < 0 ? 0 : c;
 }
 
 // KV tokens reachable through the table (Triton: n_blocks = min(cdiv(len, bs), max_blocks)).

@@ -312,34 +312,28 @@ extern "C" int ss_paged_attention_varlen_noalloc(const void* q, void* out, const
 //
 // A decode batch whose block tables all begin with the same prefix_blocks blocks
 // (prefix-cache hits share full blocks) attends that prefix once for every
-// sequence's query rows instead of once per sequence:
+// sequence's query rows instead of once per sequence, in two launches:
 //   1. the prefix is cut into S chunks of cb blocks; chunk s is a pseudo-sequence
-//      whose queries are the whole batch's (read in place, token t from row
-//      t % batch) and whose keys are the chunk, without a causal mask. The tiled
-//      prefill computes every (chunk, batch row) partial and its log-sum-exp;
-//   2. the decode attends each sequence's private suffix through its table
-//      shifted by prefix_blocks, writing the suffix part and its log-sum-exp into
-//      out;
-//   3. a combine weighs the S + 1 normalised parts by 2^(lse - max).
+//      whose keys are the chunk (its table: entries s*cb .. of the first table row,
+//      which holds the shared prefix) and whose queries are the whole batch's (read
+//      in place, token t from row t % batch), without a causal mask. The tiled
+//      prefill computes every (chunk, batch row) part, normalised, and its
+//      log-sum-exp;
+//   2. the decode attends each sequence's private suffix through its table from
+//      column prefix_blocks on (KV length seq_len - prefix tokens), leaving fp32
+//      partials; its merge completes every row, folding in the S prefix parts with
+//      weights 2^(lse - max).
 // Softmax over a union of disjoint key sets is the lse-weighted mix of the parts'
-// softmaxes, so the result is the plain decode's up to rounding.
+// softmaxes, so the result is the plain decode's up to rounding (the prefix parts
+// are stored in the head_dim type, the suffix state stays fp32).
 
 namespace {
-
-using ss::bf16_t;
-using ss::f16_t;
-using ss::f16x2;
-using ss::u32x4;
-using ss::Elem;
-using ss::fast_exp2;
-using ss::load16;
-using ss::store16;
 
 struct PrefixPlan {
   bool cascade = false;
   int cb = 0, S = 0;
-  int64_t dec = 0, work = 0, meta = 0, lse = 0, part = 0;
-  int64_t total() const { return dec + work + meta + lse + part; }
+  int64_t dec = 0, work = 0, lse = 0, part = 0, seq = 0;
+  int64_t total() const { return dec + work + lse + part + seq; }
 };
 
 int64_t round256(int64_t x) { return (x + 255) & ~(int64_t)255; }
@@ -367,114 +361,18 @@ PrefixPlan prefix_plan(int64_t batch, int n_q, int n_kv, int head_dim, int block
   const int tile_blocks = 64 / block_size > 1 ? 64 / block_size : 1;
   int64_t cb = (prefix_blocks + target - 1) / target;
   cb = (cb + tile_blocks - 1) / tile_blocks * tile_blocks;
+  // a chunk never outgrows the prefix: the chunk tables (entries s*cb .. s*cb + cb - 1
+  // of the first row, s < S) then stay below prefix_blocks + cb <= 2 * max_blocks
+  // entries, inside the table of a batch of two or more rows
+  if (cb > prefix_blocks) cb = prefix_blocks;
   pl.cb = (int)cb;
   pl.S = (int)((prefix_blocks + cb - 1) / cb);
   const int64_t elem = 2;  // bf16 / fp16
-  pl.work = round256(ss::prefill_work_bytes(pl.S, n_rep, (int)batch));
-  pl.meta = round256(4 * ((int64_t)pl.S + 1 + pl.S + batch + (int64_t)pl.S * pl.cb));
-  pl.lse = round256(4 * ((int64_t)pl.S + 1) * batch * n_q);
+  pl.work = 0;  // the prefix pass walks its (chunk, query tile) items in order
+  pl.lse = round256(4 * (int64_t)pl.S * batch * n_q);
   pl.part = round256((int64_t)pl.S * batch * n_q * head_dim * elem);
+  pl.seq = round256(batch * n_q * (int64_t)(head_dim + 2) * 4);  // fp32 rows of suffixes finished in one range
   return pl;
-}
-
-// meta = [cu: S + 1][chunk lengths: S][suffix lengths: batch][chunk tables: S * cb];
-// work = the prefill's work list: every (chunk, query tile) item costs about the same
-// (the last chunk may be shorter), so it is written in order, without the cost sort
-__global__ __launch_bounds__(256) void prefix_setup_kernel(const int32_t* __restrict__ bt,
-                                                           const int32_t* __restrict__ seq_lens, int batch, int S,
-                                                           int cb, int prefix_blocks, int block_size, int qtiles,
-                                                           int32_t* __restrict__ meta, int32_t* __restrict__ work) {
-  int32_t* cu = meta;
-  int32_t* pctx = cu + S + 1;
-  int32_t* sctx = pctx + S;
-  int32_t* ptab = sctx + batch;
-  const int n = max(max(S + 1, batch), max(S * cb, S * qtiles + 1));
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-    if (i == 0) work[0] = S * qtiles;
-    if (i < S * qtiles) work[1 + i] = ((i / qtiles) << 16) | (i % qtiles);
-    if (i <= S) cu[i] = i * batch;
-    if (i < S) pctx[i] = min(cb, prefix_blocks - i * cb) * block_size;
-    if (i < batch) sctx[i] = max(seq_lens[i] - prefix_blocks * block_size, 0);
-    // past the prefix the chunk table repeats its last block: a valid block that no
-    // key position below a chunk's length reaches
-    if (i < S * cb) ptab[i] = bt[min(i, prefix_blocks - 1)];
-  }
-}
-
-template <typename T>
-__device__ __forceinline__ float half_to_f32(uint32_t w, int hi);
-template <>
-__device__ __forceinline__ float half_to_f32<bf16_t>(uint32_t w, int hi) {
-  return __builtin_bit_cast(float, hi ? (w & 0xFFFF0000u) : (w << 16));
-}
-template <>
-__device__ __forceinline__ float half_to_f32<f16_t>(uint32_t w, int hi) {
-  return (float)__builtin_bit_cast(f16x2, w)[hi];
-}
-
-// One thread per (sequence, query head, 8 consecutive d): out = sum_i 2^(lse_i - M) o_i
-// / sum_i 2^(lse_i - M) over the suffix part (already in out) and the S prefix parts.
-template <typename T>
-__global__ __launch_bounds__(256) void prefix_combine_kernel(const T* __restrict__ part,
-                                                             const float* __restrict__ part_lse,
-                                                             const float* __restrict__ sfx_lse, T* out,
-                                                             int64_t o_sb, int64_t o_sh, int batch, int n_q,
-                                                             int head_dim, int S) {
-  const int dv = head_dim / 8;
-  const int64_t rows = (int64_t)batch * n_q;
-  const int64_t total = rows * dv;
-  for (int64_t u = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; u < total;
-       u += (int64_t)gridDim.x * blockDim.x) {
-    const int c = (int)(u % dv);
-    const int64_t bh = u / dv;
-    const int b = (int)(bh / n_q), hq = (int)(bh - (int64_t)b * n_q);
-    T* o = out + b * o_sb + hq * o_sh + 8 * c;
-    // running (max, weight sum, weighted output) from the suffix part; an empty suffix
-    // (lse -inf) starts from nothing. Every chunk holds at least one key, so the max is
-    // finite after the first batch and a -inf part weighs exactly 0.
-    const float ls = sfx_lse[bh];
-    const bool has_sfx = ls > -__builtin_inff();
-    const u32x4 vs = load16(o);
-    float acc[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      acc[2 * e] = has_sfx ? half_to_f32<T>(vs[e], 0) : 0.f;
-      acc[2 * e + 1] = has_sfx ? half_to_f32<T>(vs[e], 1) : 0.f;
-    }
-    float m = ls, wsum = has_sfx ? 1.f : 0.f;
-    // prefix parts four at a time: all loads of a batch issued before any is used
-    for (int s0 = 0; s0 < S; s0 += 4) {
-      float lv[4];
-      u32x4 v[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t i = (int64_t)min(s0 + j, S - 1) * rows + bh;
-        lv[j] = part_lse[i];
-        v[j] = load16(part + i * head_dim + 8 * c);
-      }
-      float mx = m;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) mx = s0 + j < S ? fmaxf(mx, lv[j]) : mx;
-      const float keep = fast_exp2(m - mx);
-      wsum *= keep;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] *= keep;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float w = s0 + j < S ? fast_exp2(lv[j] - mx) : 0.f;
-        wsum += w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc[2 * e] += w * half_to_f32<T>(v[j][e], 0);
-          acc[2 * e + 1] += w * half_to_f32<T>(v[j][e], 1);
-        }
-      }
-      m = mx;
-    }
-    const float inv = 1.f / wsum;
-    store16(o, u32x4{Elem<T>::pack2(acc[0] * inv, acc[1] * inv), Elem<T>::pack2(acc[2] * inv, acc[3] * inv),
-                     Elem<T>::pack2(acc[4] * inv, acc[5] * inv), Elem<T>::pack2(acc[6] * inv, acc[7] * inv)});
-  }
 }
 
 }  // namespace
@@ -552,28 +450,18 @@ extern "C" int ss_paged_attention_shared_prefix(const void* q, void* out, const 
     return run(p, dtype, head_dim, 1, ws, pl.dec + pl.work, s, dec, !dec);
   }
 
-  int32_t* meta = (int32_t*)(ws + pl.dec + pl.work);
-  float* lse = (float*)(ws + pl.dec + pl.work + pl.meta);
-  void* part = ws + pl.dec + pl.work + pl.meta + pl.lse;
-  const int64_t rows = batch * n_q;
-  int32_t* work = (int32_t*)(ws + pl.dec);
+  float* lse = (float*)(ws + pl.dec + pl.work);
+  void* part = ws + pl.dec + pl.work + pl.lse;
+  float* seq_o = (float*)(ws + pl.dec + pl.work + pl.lse + pl.part);
+  float* seq_ml = seq_o + batch * n_q * (int64_t)head_dim;
   const int qtiles = (int)((batch * p.n_rep + 127) / 128);
-  {
-    const int64_t n = std::max<int64_t>(std::max<int64_t>(pl.S + 1, batch),
-                                        std::max<int64_t>((int64_t)pl.S * pl.cb, (int64_t)pl.S * qtiles + 1));
-    hipLaunchKernelGGL(prefix_setup_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, block_tables,
-                       seq_lens, (int)batch, pl.S, pl.cb, prefix_blocks, block_size, qtiles, meta, work);
-    if ((st = ss_host::launch_status("shared-prefix setup")) != SS_OK) return st;
-  }
-  const int32_t* cu = meta;
-  const int32_t* pctx = cu + pl.S + 1;
-  const int32_t* sctx = pctx + pl.S;
-  const int32_t* ptab = sctx + batch;
   {  // 1. prefix chunks as pseudo-sequences of the prefill, queries read in place
     AttnParams pp = {};
-    fill_common(pp, q, part, k_cache, v_cache, ptab, pctx, pl.S, n_q, n_kv, pl.cb, block_size, num_blocks,
-                c_strides, pl.cb, scale);
-    pp.cu = cu;
+    fill_common(pp, q, part, k_cache, v_cache, block_tables, nullptr, pl.S, n_q, n_kv, pl.cb, block_size,
+                num_blocks, c_strides, pl.cb, scale);
+    pp.chunk_tokens = pl.cb * block_size;
+    pp.prefix_tokens = prefix_blocks * block_size;
+    pp.work_qtiles = qtiles;
     pp.q_sb = 0;
     pp.q_st = q_strides[0];
     pp.q_sh = q_strides[1];
@@ -584,35 +472,26 @@ extern "C" int ss_paged_attention_shared_prefix(const void* q, void* out, const 
     pp.lse = lse;
     pp.noncausal = 1;
     pp.q_period = (int)batch;
-    st = ss::launch_prefill(pp, dtype, head_dim, (int)batch, work, pl.work, s, true);
+    st = ss::launch_prefill(pp, dtype, head_dim, (int)batch, nullptr, 0, s, true);
     if (st != SS_OK) return st;
   }
-  {  // 2. private suffixes: the table from column prefix_blocks on
-    AttnParams ps = p;
-    ps.bt = block_tables + prefix_blocks;
-    ps.max_blocks = max_blocks - prefix_blocks;
-    ps.ctx_lens = sctx;
-    ps.lse = lse + (int64_t)pl.S * rows;
-    ps.rmax = ss::decode_rows_for(1, ps.n_rep);
-    // suffixes are short (C4: about nine 32-key pairs each): one range per CU and head
-    // group at most (measured 47.6 us at C4 against 51.1 us for two; 192 and 128 ranges
-    // were slower)
-    ps.range_cap = ss_host::device_cu_count();
-    st = ss::launch_decode(ps, dtype, head_dim, 1, ws, pl.dec, s);
-    if (st != SS_OK) return st;
-  }
-  // 3. combine
-  const int64_t threads = rows * (head_dim / 8);
-  const int grid = (int)std::min<int64_t>((threads + 255) / 256, 8192);
-  if (dtype == SS_DTYPE_BF16)
-    hipLaunchKernelGGL(prefix_combine_kernel<bf16_t>, dim3(grid), dim3(256), 0, s, (const bf16_t*)part, lse,
-                       lse + (int64_t)pl.S * rows, (bf16_t*)out, o_strides[0], o_strides[1], (int)batch, n_q,
-                       head_dim, pl.S);
-  else
-    hipLaunchKernelGGL(prefix_combine_kernel<f16_t>, dim3(grid), dim3(256), 0, s, (const f16_t*)part, lse,
-                       lse + (int64_t)pl.S * rows, (f16_t*)out, o_strides[0], o_strides[1], (int)batch, n_q,
-                       head_dim, pl.S);
-  return ss_host::launch_status("shared-prefix combine");
+  // 2. private suffixes: the table from column prefix_blocks on, lengths past the
+  // prefix; the prefix parts are folded in where each row is finished
+  AttnParams ps = p;
+  ps.bt = block_tables + prefix_blocks;
+  ps.max_blocks = max_blocks - prefix_blocks;
+  ps.ctx_shift = prefix_blocks * block_size;
+  ps.rmax = ss::decode_rows_for(1, ps.n_rep);
+  ps.px_part = part;
+  ps.px_lse = lse;
+  ps.px_n = pl.S;
+  ps.px_seq_o = seq_o;
+  ps.px_seq_ml = seq_ml;
+  // suffixes are short (C4: about nine 32-key pairs each): one range per CU and head
+  // group at most (measured 47.6 us at C4 against 51.1 us for two; 192 and 128 ranges
+  // were slower)
+  ps.range_cap = ss_host::device_cu_count();
+  return ss::launch_decode(ps, dtype, head_dim, 1, ws, pl.dec, s);
 }
 
 extern "C" int ss_attention_status(int* flags, int clear, void* stream) {

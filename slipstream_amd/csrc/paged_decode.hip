@@ -77,7 +77,7 @@ __device__ __forceinline__ int decode_pairs(const AttnParams& p, int b) {
   int64_t qoff;
   seq_queries(p, b, qlen, qoff);
   if (!is_decode_seq(p, qlen)) return 0;
-  const int kvt = seq_kv_tokens(p, p.ctx_lens[b]);
+  const int kvt = seq_kv_tokens(p, kv_len(p, b));
   return (kvt + kPairTokens - 1) / kPairTokens;
 }
 
@@ -150,6 +150,51 @@ struct RowState {
   float m;          // running max (log2 domain), uniform over the lanes of a row
   float l;          // this lane's partial sum of exp2(s - m)
 };
+
+// Shared-prefix cascade: fold the p.px_n normalised prefix parts of query row
+// `row` (b * n_q + hq) into a running state -- max m and sum l (log2 domain), the
+// unnormalised output o[2c], o[2c + 1] of the 8 consecutive d at d0 + 8c -- as
+// parts of weight 2^(lse_s - M) against the state's 2^(m - M): the softmax over a
+// union of disjoint key sets is the lse-weighted mix of the parts' softmaxes.
+// The loads of SB parts are issued before any is used. Every part holds at least
+// one key (finite lse), so M is finite after the first batch.
+template <typename T, int D, int NC, int SB>
+__device__ __forceinline__ void fold_prefix(const AttnParams& p, int64_t row, int d0, float& m, float& l,
+                                            f32x4 (&o)[2 * NC]) {
+  const int64_t rows = (int64_t)p.batch * p.n_q;
+  const T* part = (const T*)p.px_part;
+  for (int s0 = 0; s0 < p.px_n; s0 += SB) {
+    float lv[SB];
+    u32x4 v[SB][NC];
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const int64_t i = (int64_t)min(s0 + j, p.px_n - 1) * rows + row;
+      lv[j] = p.px_lse[i];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) v[j][c] = load16(part + i * D + d0 + 8 * c);
+    }
+    float mx = m;
+#pragma unroll
+    for (int j = 0; j < SB; ++j) mx = s0 + j < p.px_n ? fmaxf(mx, lv[j]) : mx;
+    const float keep = fast_exp2(m - mx);
+    l *= keep;
+#pragma unroll
+    for (int c = 0; c < 2 * NC; ++c) o[c] *= keep;
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const float w = s0 + j < p.px_n ? fast_exp2(lv[j] - mx) : 0.f;
+      l += w;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        o[2 * c] += w * f32x4{Elem<T>::lo(v[j][c][0]), Elem<T>::hi(v[j][c][0]), Elem<T>::lo(v[j][c][1]),
+                              Elem<T>::hi(v[j][c][1])};
+        o[2 * c + 1] += w * f32x4{Elem<T>::lo(v[j][c][2]), Elem<T>::hi(v[j][c][2]), Elem<T>::lo(v[j][c][3]),
+                                  Elem<T>::hi(v[j][c][3])};
+      }
+    }
+    m = mx;
+  }
+}
 
 // lim_min: the smallest per-row key limit of this wave's rows (wave-uniform). A pair
 // whose tiles are both valid and end at or before lim_min needs no masking.
@@ -330,7 +375,10 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
   const int s_w = wr * chunk;
   const int e_w = min(s_w + chunk, total);
   if (s_w >= e_w) {
-    if (tid == 0) rec[0] = -1;
+    if (tid == 0) {
+      rec[0] = -1;
+      rec[5] = -1;
+    }
     return;
   }
   if (tid == 0) s_b0 = -1;
@@ -358,13 +406,14 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) voff_v[e] = (4 * g + e) * tok_bytes + h * head_bytes + 16 * (n < Tile::NCH ? n : 0);
   int rec_b = -1, rec_cb = 0, rec_cb1 = 0, rec_slot = 0;
+  int rec_c0 = -1, rec_c1 = -1;  // sequences [rec_c0, rec_c1) finished here, cascade only
   // Write a finished segment: the output rows when it covers the whole sequence,
   // else an unnormalised partial (max, sum, acc) for the merge kernel.
   auto finish = [&](int b, int c, int64_t qoff, int j, int hq, bool row_ok, int seg0, int seg1, int nbp,
                     const RowState<T, D>& st) {
   const float lt = sum_across_rows(st.l);
       const bool complete = seg0 == 0 && seg1 == nbp;
-      if (complete) {
+      if (complete && p.px_n == 0) {
         if (row_ok) {
           const float inv = lt > 0.f ? 1.f / lt : 0.f;
           if (p.lse && g == 0) p.lse[lse_index(p, b, qoff, j, hq)] = row_lse(st.m, lt);
@@ -386,10 +435,13 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
           }
         }
       } else {
+        // a partial: this range's piece of a split sequence, or (shared-prefix cascade)
+        // a sequence finished here, which the merge completes with the prefix parts
         const int slot = c > s_w ? 1 : 0;
-        const int64_t pidx = (((int64_t)blockIdx.x * 2 + slot) * p.hpw + wave) * p.rmax + n;
+        const int64_t pidx = complete ? lse_index(p, b, qoff, j, hq)
+                                      : (((int64_t)blockIdx.x * 2 + slot) * p.hpw + wave) * p.rmax + n;
         if (row_ok) {
-          float* po = p.ws_o + pidx * D;
+          float* po = (complete ? p.px_seq_o : p.ws_o) + pidx * D;
 #pragma unroll
           for (int mt = 0; mt < Tile::MT; ++mt) {
             const int dbase = 128 * mt + 32 * g;
@@ -405,11 +457,15 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
             }
           }
           if (g == 0) {
-            p.ws_ml[pidx * 2] = st.m;
-            p.ws_ml[pidx * 2 + 1] = lt;
+            float* pml = (complete ? p.px_seq_ml : p.ws_ml) + pidx * 2;
+            pml[0] = st.m;
+            pml[1] = lt;
           }
         }
-        if (c >= s_w) {
+        if (complete) {
+          rec_c0 = rec_c0 < 0 ? b : rec_c0;
+          rec_c1 = b + 1;
+        } else if (c >= s_w) {
           rec_b = b;
           rec_cb = c;
           rec_cb1 = c + nbp;
@@ -437,7 +493,7 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
       return t2;
     };
     auto seq_kvt = [&](int bb) {
-      const int cx = __builtin_amdgcn_readfirstlane(p.ctx_lens[bb] < 0 ? 0 : p.ctx_lens[bb]);
+      const int cx = __builtin_amdgcn_readfirstlane(kv_len(p, bb));
       return seq_kv_tokens(p, cx);
     };
     // this lane's query row of sequence bb: (row ok, token j, query head)
@@ -494,7 +550,7 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
         tcn = seq_ctx(nb, kvt_n);
         fetch_phys(p, tcn, 0, phn);
       }
-      const int lim = row_ok ? (__builtin_amdgcn_readfirstlane(p.ctx_lens[b] < 0 ? 0 : p.ctx_lens[b])) - qlen + j + 1 : 0;
+      const int lim = row_ok ? __builtin_amdgcn_readfirstlane(kv_len(p, b)) - qlen + j + 1 : 0;
       const int lim_eff = lim < kvt ? lim : kvt;
       int lim_min = row_ok ? lim_eff : 0x7fffffff;
 #pragma unroll
@@ -569,7 +625,7 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
       }
       const int seg0 = pos - c;
       const int seg1 = min(e_w - c, nbp);
-      const int ctx = __builtin_amdgcn_readfirstlane(p.ctx_lens[b] < 0 ? 0 : p.ctx_lens[b]);
+      const int ctx = __builtin_amdgcn_readfirstlane(kv_len(p, b));
       const int kvt = seq_kv_tokens(p, ctx);
       const int R = qlen * p.n_rep;
       const bool row_ok = n < R;
@@ -624,6 +680,8 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
     rec[2] = rec_cb1;
     rec[3] = rec_slot;
     rec[4] = chunk;
+    rec[5] = rec_c0;
+    rec[6] = rec_c1;
   }
 }
 
@@ -635,9 +693,11 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
 //    whose sequence is longer than max_query_len has: zeros, and the status word
 //    gets kStatusQueryTooLong, so a broken promise never leaves rows unwritten.
 // A packed stream whose cu_seqlens run past total_tokens raises kStatusStreamOverrun
-// (seq_queries has clamped it).
+// (seq_queries has clamped it); a shared-prefix call whose prefix is longer than a
+// sequence raises kStatusPrefixShort (its suffix counts as empty). In a shared-prefix
+// call the merge also folds the prefix parts into the rows it writes.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void decode_merge_kernel(const AttnParams p, int n_wg) {
+__global__ __launch_bounds__(512) void decode_merge_kernel(const AttnParams p, int n_wg) {
   const int tid = threadIdx.x;
   if ((int)blockIdx.x >= n_wg) {
     const int b = blockIdx.x - n_wg;
@@ -646,11 +706,30 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const AttnParams p, i
     seq_queries(p, b, qlen, qoff);
     if (p.cu && tid == 0 && (p.cu[b + 1] > p.total_tokens || p.cu[b] > p.cu[b + 1] || p.cu[b] < 0))
       atomicOr(&g_status, kStatusStreamOverrun);
+    if (p.px_n > 0 && tid == 0 && p.ctx_lens[b] < p.ctx_shift) atomicOr(&g_status, kStatusPrefixShort);
     if (qlen <= 0) return;
     const int R = qlen * p.n_rep;
     int covered;  // rows r = j * n_rep + i (per KV head) some kernel writes
     if (is_decode_seq(p, qlen)) {
       if (decode_pairs(p, b) != 0) return;
+      if constexpr (D <= 128) {
+        if (p.px_n > 0) {  // shared-prefix cascade, no suffix key: the prefix parts alone
+          constexpr int DV = D / 8;
+          for (int u = tid; u < qlen * p.n_q * DV; u += blockDim.x) {
+            const int c = u % DV, jh = u / DV;
+            const int j = jh / p.n_q, hq = jh - j * p.n_q;
+            float m = kNegBig, l = 0.f;
+            f32x4 ov[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+            fold_prefix<T, D, 1, 8>(p, (int64_t)b * p.n_q + hq, 8 * c, m, l, ov);
+            const float inv = l > 0.f ? 1.f / l : 0.f;
+            if (p.lse && c == 0) p.lse[lse_index(p, b, qoff, j, hq)] = row_lse(m, l);
+            T* o = (T*)p.out + (int64_t)b * p.o_sb + (qoff + j) * p.o_st + (int64_t)hq * p.o_sh + 8 * c;
+            store16(o, u32x4{Elem<T>::pack2(ov[0][0] * inv, ov[0][1] * inv), Elem<T>::pack2(ov[0][2] * inv, ov[0][3] * inv),
+                             Elem<T>::pack2(ov[1][0] * inv, ov[1][1] * inv), Elem<T>::pack2(ov[1][2] * inv, ov[1][3] * inv)});
+          }
+          return;
+        }
+      }
       covered = 0;
     } else {
       covered = min(R, p.row_cap);
@@ -671,10 +750,34 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const AttnParams p, i
     return;
   }
   const int* rec = p.ws_rec + (int64_t)blockIdx.x * 8;
+  const int hg = blockIdx.x % p.n_hgroups;
+  if constexpr (D <= 128) {
+    const int c0 = rec[5], c1 = rec[6];
+    if (p.px_n > 0 && c0 >= 0) {
+      // shared-prefix cascade: the sequences this range finished (one query token
+      // each), completed with the prefix parts; one thread per (sequence, query head
+      // of the head group, 8 consecutive d)
+      constexpr int DV = D / 8;
+      const int hrows = p.hpw * p.n_rep;
+      for (int u = tid; u < (c1 - c0) * hrows * DV; u += blockDim.x) {
+        const int c = u % DV, t = u / DV;
+        const int bb = c0 + t / hrows, hq = hg * hrows + t % hrows;
+        const int64_t row = (int64_t)bb * p.n_q + hq;
+        float m = p.px_seq_ml[row * 2], l = p.px_seq_ml[row * 2 + 1];
+        const f32x4* po = reinterpret_cast<const f32x4*>(p.px_seq_o + row * D + 8 * c);
+        f32x4 ov[2] = {po[0], po[1]};
+        fold_prefix<T, D, 1, 8>(p, row, 8 * c, m, l, ov);
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        if (p.lse && c == 0) p.lse[row] = row_lse(m, l);
+        T* o = (T*)p.out + (int64_t)bb * p.o_sb + (int64_t)hq * p.o_sh + 8 * c;
+        store16(o, u32x4{Elem<T>::pack2(ov[0][0] * inv, ov[0][1] * inv), Elem<T>::pack2(ov[0][2] * inv, ov[0][3] * inv),
+                         Elem<T>::pack2(ov[1][0] * inv, ov[1][1] * inv), Elem<T>::pack2(ov[1][2] * inv, ov[1][3] * inv)});
+      }
+    }
+  }
   const int b = rec[0];
   if (b < 0) return;
   const int cb1 = rec[2], slot0 = rec[3], chunk = rec[4];
-  const int hg = blockIdx.x % p.n_hgroups;
   const int wr0 = blockIdx.x / p.n_hgroups;
   const int wr1 = (cb1 - 1) / chunk;
   int qlen;
@@ -726,9 +829,17 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const AttnParams p, i
       }
       mmax = mx;
     }
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
     const int j = r / p.n_rep;
     const int hq = (hg * p.hpw + wave) * p.n_rep + (r - j * p.n_rep);
+    if constexpr (D <= 128) {
+      if (p.px_n > 0) {  // shared-prefix cascade: fold in the prefix parts of the row
+        f32x4 ov[2] = {o0, o1};
+        fold_prefix<T, D, 1, 8>(p, (int64_t)b * p.n_q + hq, 8 * c, mmax, lsum, ov);
+        o0 = ov[0];
+        o1 = ov[1];
+      }
+    }
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
     if (p.lse && c == 0) p.lse[lse_index(p, b, qoff, j, hq)] = row_lse(mmax, lsum);
     T* o = (T*)p.out + (int64_t)b * p.o_sb + (qoff + j) * p.o_st + (int64_t)hq * p.o_sh + 8 * c;
     store16(o, u32x4{Elem<T>::pack2(o0[0] * inv, o0[1] * inv), Elem<T>::pack2(o0[2] * inv, o0[3] * inv),
@@ -837,7 +948,10 @@ static int launch_decode_typed(AttnParams p, int max_query_len, char* ws, int64_
                        p);
   int st = ss_host::launch_status("paged attention decode");
   if (st != SS_OK) return st;
-  hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(n_wg + p.batch), dim3(256), 0, stream, p, n_wg);
+  // a shared-prefix merge folds S prefix parts into each of its rows' 8-d pieces (28 x
+  // 16 per C4 sequence): 512 threads give every piece its own thread
+  const int merge_threads = p.px_n > 0 ? 512 : 256;
+  hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(n_wg + p.batch), dim3(merge_threads), 0, stream, p, n_wg);
   return ss_host::launch_status("paged attention decode merge");
 }
 

@@ -61,7 +61,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const AttnParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
-  const int ctx = p.ctx_lens[b] < 0 ? 0 : p.ctx_lens[b];
+  const int ctx = kv_len(p, b);
   const int kvt = seq_kv_tokens(p, ctx);
   const int last_row = min(R - 1, row0 + C::ROWS - 1);
   const int kv_end = min(kvt, ctx - qlen + last_row / p.n_rep + 1);
@@ -370,13 +370,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // e * n_kv + h, one per KV head) in snake order: round r takes item r*G + j, or
   // r*G + G-1-j in odd rounds, so a workgroup that drew a long item early draws a
   // short one next.
-  const int total = __builtin_amdgcn_readfirstlane(work[0]) * p.n_kv;
+  // (With p.work_qtiles > 0 the entries are every (sequence, tile) in order, equal in
+  // cost up to the last sequence's, and no list is read.)
+  const int wq = p.work_qtiles;
+  const int total = (wq > 0 ? p.batch * wq : __builtin_amdgcn_readfirstlane(work[0])) * p.n_kv;
   const int G = gridDim.x, wg = blockIdx.x;
   for (int round = 0; round * G < total; ++round) {
     const int idx = round * G + ((round & 1) ? G - 1 - wg : wg);
     if (idx >= total) continue;
     const int entry = idx / p.n_kv;
-    const int bq = __builtin_amdgcn_readfirstlane(work[1 + entry]);
+    const int bq = wq > 0 ? ((entry / wq) << 16) | (entry % wq) : __builtin_amdgcn_readfirstlane(work[1 + entry]);
     [&](const int b, const int qt, const int h) {
   int qlen;
   int64_t qoff;
@@ -394,7 +397,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = wave & 3;  // the 16-key group whose K (waves 0-3) or V (4-7) this wave loads
   const int n = lane & 15, g = lane >> 4;
-  const int ctx = __builtin_amdgcn_readfirstlane(p.ctx_lens[b] < 0 ? 0 : p.ctx_lens[b]);
+  const int ctx = __builtin_amdgcn_readfirstlane(kv_len(p, b));
   const int kvt = seq_kv_tokens(p, ctx);
   const int last_row = min(R - 1, row0 + ROWS - 1);
   const int kv_end = p.noncausal ? kvt : min(kvt, ctx - qlen + last_row / p.n_rep + 1);
@@ -759,7 +762,7 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const AttnParams p, 
     if (qlen <= 0 || is_decode_seq(p, qlen)) return -1;
     const int R = qlen * p.n_rep, row0 = qt * 128;
     if (row0 >= R) return -1;
-    const int ctx = p.ctx_lens[b] < 0 ? 0 : p.ctx_lens[b];
+    const int ctx = kv_len(p, b);
     const int kvt = seq_kv_tokens(p, ctx);
     const int last_row = min(R - 1, row0 + 127);
     const int kv_end = p.noncausal ? kvt : min(kvt, ctx - qlen + last_row / p.n_rep + 1);
@@ -811,8 +814,13 @@ int launch_prefill_typed(const AttnParams& p, int max_query_len, int* work, int6
                          (long long)qtiles, p.batch);
       return SS_ERR_UNSUPPORTED;
     }
-    const int64_t need = prefill_work_bytes(p.batch, p.n_rep, max_query_len);
-    if (!work || work_bytes < need) {
+    const int64_t need = p.work_qtiles > 0 ? 0 : prefill_work_bytes(p.batch, p.n_rep, max_query_len);
+    if (p.work_qtiles > 0 && p.work_qtiles != qtiles) {
+      ss_host::set_error("paged attention prefill: %d implicit query tiles, the launch has %lld", p.work_qtiles,
+                         (long long)qtiles);
+      return SS_ERR_INVALID;
+    }
+    if (need > 0 && (!work || work_bytes < need)) {
       ss_host::set_error("paged attention prefill: workspace of %lld bytes for the work list, needs %lld",
                          (long long)work_bytes, (long long)need);
       return SS_ERR_WORKSPACE;
@@ -828,7 +836,7 @@ int launch_prefill_typed(const AttnParams& p, int max_query_len, int* work, int6
       }
       attr_set = true;
     }
-    if (!planned) {
+    if (!planned && p.work_qtiles == 0) {
       hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPlanBuckets), 0, stream, p, work, (int)qtiles);
       int st = ss_host::launch_status("paged attention prefill plan");
       if (st != SS_OK) return st;

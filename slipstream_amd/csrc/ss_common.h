@@ -27,7 +27,7 @@ constexpr float kNegBig = -1.0e30f;
 constexpr float kLog2e = 1.4426950408889634f;
 
 // 16-bit element traits: MFMA 16x16x32 with fp32 accumulation, packing of two
-// fp32 values into one dword of this type, and conversion of one value.
+// fp32 values into one dword of this type and unpacking them again.
 template <typename T>
 struct Elem;
 
@@ -41,6 +41,9 @@ struct Elem<bf16_t> {
     bf16x2 v = {(bf16_t)lo, (bf16_t)hi};  // v_cvt_pk_bf16_f32, round to nearest even
     return __builtin_bit_cast(uint32_t, v);
   }
+  // the low / high element of a packed pair, exactly
+  static __device__ __forceinline__ float lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
 };
 
 template <>
@@ -53,6 +56,8 @@ struct Elem<f16_t> {
     f16x2 v = {(f16_t)lo, (f16_t)hi};
     return __builtin_bit_cast(uint32_t, v);
   }
+  static __device__ __forceinline__ float lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w)[0]; }
+  static __device__ __forceinline__ float hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2, w)[1]; }
 };
 
 // Byte-select of two dwords: result = (lo16 of `a` half ha, hi16 = `b` half hb),

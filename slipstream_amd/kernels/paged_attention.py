@@ -180,8 +180,9 @@ def paged_attention_shared_prefix(
     ``paged_attention_decode`` (``kernels/paged_attention.py:21-40``) returns, up to
     rounding, while reading the shared prefix once for the batch instead of once per
     sequence. The caller promises ``block_tables[:, :prefix_blocks]`` equal to row 0 in
-    every row and ``seq_lens >= prefix_blocks * block_size``; neither is checked on the
-    device (``SLIPSTREAM_DEBUG`` checks both on the host)."""
+    every row (the prefix pass reads row 0) and ``seq_lens >= prefix_blocks *
+    block_size`` (a shorter sequence sets ``SS_STATUS_PREFIX_SHORT`` in
+    ``attention_status``); ``SLIPSTREAM_DEBUG`` checks both on the host."""
     if q.ndim != 4 or q.shape[2] != 1:
         raise ValueError(f"q must be [B, n_q, 1, D], got {tuple(q.shape)}")
     batch, n_q, _, head_dim = q.shape
@@ -301,8 +302,10 @@ def _check_stream(cu: torch.Tensor, total: int, max_query_len: int) -> None:
 def attention_status(device: torch.device | int | None = None, clear: bool = True) -> int:
     """The device status word (``ss_attention_status``) after the current stream's work:
     ``SS_STATUS_QUERY_TOO_LONG`` (a packed sequence longer than ``max_query_len``, its
-    extra rows written as zeros) and ``SS_STATUS_STREAM_OVERRUN`` (``cu_seqlens`` past
-    the token count, clamped). Synchronises the stream; 0 means no promise was broken."""
+    extra rows written as zeros), ``SS_STATUS_STREAM_OVERRUN`` (``cu_seqlens`` past
+    the token count, clamped) and ``SS_STATUS_PREFIX_SHORT`` (a shared-prefix call
+    whose prefix is longer than a sequence). Synchronises the stream; 0 means no
+    promise was broken."""
     dev = torch.device("cuda", torch.cuda.current_device() if device is None else
                        (device if isinstance(device, int) else device.index or 0))
     flags = _ffi.ctypes.c_int(0)

@@ -1,5 +1,6 @@
-"""GPU parity of the shared-prefix decode (prefix pass + suffix decode + log-sum-exp
-combine) against the numpy oracle of ``paged_attention_ref`` (``attention_ref.py:68-89``).
+"""GPU parity of the shared-prefix decode (prefix pass, then the suffix decode whose merge
+folds in the prefix parts by log-sum-exp weight) against the numpy oracle of
+``paged_attention_ref`` (``attention_ref.py:68-89``).
 
 The cascade reorders the softmax sum (prefix chunks and the suffix are normalised apart,
 then mixed by ``2^(lse - max)``), so it matches the oracle to the attention tolerance, not
@@ -15,7 +16,8 @@ import torch
 
 from oracle import paged_attention as ora
 from slipstream_amd import workloads
-from slipstream_amd.kernels import paged_attention_decode, paged_attention_shared_prefix
+from slipstream_amd._ffi import SS_STATUS_PREFIX_SHORT
+from slipstream_amd.kernels import attention_status, paged_attention_decode, paged_attention_shared_prefix
 from tests._helpers import assert_attn_close, f64, oracle_paged_rows, tables_array
 
 pytestmark = pytest.mark.gpu
@@ -132,3 +134,23 @@ def test_rejects_bad_prefix(device):
     with pytest.raises(ValueError, match="q must be"):
         paged_attention_shared_prefix(b.padded_q().expand(-1, -1, 2, -1), b.kv_cache, b.block_tables,
                                       b.context_lens, 0, b.scale, 16, 4)
+
+
+def test_sequence_shorter_than_prefix_is_flagged(device, monkeypatch):
+    """A sequence with fewer KV tokens than the shared prefix breaks the caller's promise:
+    the call still writes defined values (that row's suffix counts as empty) and sets
+    SS_STATUS_PREFIX_SHORT; the other rows keep their exact result, and a call that keeps
+    the promise leaves the word clear."""
+    monkeypatch.delenv("SLIPSTREAM_DEBUG", raising=False)
+    b = workloads.prefix_share(device=device, seed=3, batch=32)
+    attention_status(clear=True)
+    _run(b, b.shared_blocks)
+    assert attention_status(clear=True) == 0
+    lens = b.context_lens.clone()
+    lens[5] = b.shared_blocks * 16 - 7
+    out = paged_attention_shared_prefix(b.padded_q(), b.kv_cache, b.block_tables, lens, 0, b.scale, 16,
+                                        b.shared_blocks)
+    assert attention_status(clear=True) & SS_STATUS_PREFIX_SHORT
+    rows = [i for i in range(b.batch) if i != 5]
+    assert_attn_close(out[rows], _oracle(b, rows), "rows that keep the promise")
+    assert torch.isfinite(out[5].float()).all()
