@@ -472,6 +472,12 @@ __global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
 //     row's 64 contiguous bytes. Prefetches past the range use an offset past the
 //     end of the buffer: they return zeros without touching memory, and the loop
 //     needs no branch.
+//   - The loop is VALU-bound rather than MFMA- or memory-bound: per stage and wave
+//     (MT = NS = 4) 64 MFMAs against about 340 VALU instructions -- the nibble
+//     unpack (8 per 32-bit word), the fold (2 FMAs per accumulator element) and the
+//     activation staging. With loads and stores taken out it still took 48 us of the
+//     4096 x 28672, m = 256 linear's 101 us; prefetching activations PF stages ahead
+//     as well changed nothing.
 //   - Per 32-key step the MFMA accumulates G = sum x (MAGIC + q) for every
 //     (activation tile, weight tile) pair; one fold per stage:
 //       acc += s * G - s * (MAGIC + z) * X.
@@ -1078,12 +1084,17 @@ struct W4Plan {
 // Tiled kernel for m >= 2 when g % 128 == 0 and K is a whole number of PF-stage
 // rounds. Shapes (activation tiles MT, weight tiles NS per wave, prefetch depth PF)
 // by m: the bandwidth-bound sizes keep eight stages of weights in flight per wave;
-// m > 64 (MFMA-bound) takes 64 x 64 wave tiles. The K split aims at two
-// workgroups per CU (one for m > 64), each range at least one round of PF stages,
-// with the workgroup's scale table within kTileTableMax bytes of LDS; the
-// partials take ks * m * n floats of workspace. The cap keeps two workgroups per
-// CU: with the 35 KB activation stages of m > 32, a 64 KB table left room for one
-// (a 4096 x 28672 linear at m = 256 took 233 us instead of 2 x 67 us).
+// m > 64 takes 64 x 64 wave tiles. The K split aims at one workgroup
+// per CU for m <= 64 and two for m > 64, in ranges of equal length (the split
+// count divides the rounds of PF stages), with the workgroup's scale table within
+// kTileTableMax bytes of LDS; the partials take ks * m * n floats of workspace.
+// Measured over the Llama-3-8B linears (kernel + reduce), e.g. 4096 x 6144 at
+// m = 64: 19.9 us for 4 ranges against 22.9 us for 8 and 22.7 us for 3 uneven
+// ones; 4096 x 28672 at m = 64: 39.9 us unsplit against 46.6 us for 3 ranges;
+// 14336 x 4096 at m = 256: 56.4 us for 8 ranges against 66.0 us for 4. The
+// table cap keeps two workgroups per CU: with the 35 KB activation stages of
+// m > 32, a 64 KB table left room for one (a 4096 x 28672 linear at m = 256 took
+// 233 us instead of 2 x 67 us).
 constexpr int kTileTableMax = 40 * 1024;
 
 size_t tile_table_bytes(int ns, int kchunk, int g) {
@@ -1112,11 +1123,12 @@ bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
   const int64_t n_tiles = (n + 64 * ns - 1) / (64 * ns);
   const int64_t m_blocks = (m + 16 * mt - 1) / (16 * mt);
   if (n_tiles > 65535 || m_blocks > 65535) return false;
-  const int64_t target = (m <= 64 ? 2LL : 1LL) * ss_host::device_cu_count();
+  const int64_t target = (m <= 64 ? 1LL : 2LL) * ss_host::device_cu_count();
   const int64_t tiles = n_tiles * m_blocks;
   const int64_t rounds = iters / pf;
   int64_t ks = (target + tiles - 1) / tiles;
   ks = ks < 1 ? 1 : (ks > rounds ? rounds : ks);
+  while (ks > 1 && rounds % ks) --ks;  // equal ranges
   if (ks > 65535) return false;
   // more ranges while a range's scale table is too large; the ranges stay balanced
   int64_t per = (rounds + ks - 1) / ks;
