@@ -486,7 +486,7 @@ constexpr int kOutOfRange = 0x40000000;  // buffer offset past any operand (< 2^
 
 template <typename T, int MT, int NS, int PF>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void w4a16_tile_kernel(
-    const W4Params p, float* __restrict__ part, int kchunk) {
+    const W4Params p, float* __restrict__ part, int kchunk, int ks, int n_tiles, int m_blocks) {
   typedef W4Elem<T> E;
   constexpr int BM = 16 * MT;
   constexpr int LROW = 128 + 8;  // LDS row of an activation stage, elements (16-byte skew)
@@ -498,13 +498,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ln = lane & 15, kg = lane >> 4;
-  // grid (K ranges, weight tiles, activation tiles): the ranges of one tile are
-  // dispatched together, so the resident workgroups read whole weight rows
-  // (adjacent ranges) rather than one range of every row
-  const int zr = blockIdx.x;
-  const int nb = blockIdx.y * 64 * NS;  // the workgroup's first weight row
+  // workgroup -> (K range, weight tile, activation tile). Workgroups go to the eight
+  // XCDs round robin, so ids 8 apart share an XCD and its L2: the m_blocks activation
+  // tiles of one (range, weight tile) pair get ids 8 apart and are dispatched together,
+  // and the weight tile they all read comes from that L2 after the first read (in
+  // (range, tile, m) order the pairs' m_blocks reads were a whole grid apart and each
+  // came from HBM). The ranges of one weight tile are adjacent pairs, so the resident
+  // workgroups read whole weight rows. Ids past the last pair (padding of the last group
+  // of eight) exit.
+  const int blk = blockIdx.x / (8 * m_blocks), within = blockIdx.x - blk * 8 * m_blocks;
+  const int pair = blk * 8 + (within & 7);
+  if (pair >= ks * n_tiles) return;
+  const int zr = pair % ks;
+  const int nb = (pair / ks) * 64 * NS;  // the workgroup's first weight row
   const int n0 = nb + wave * 16 * NS;   // this wave's
-  const int m0 = blockIdx.z * BM;
+  const int m0 = (within >> 3) * BM;
   const int rows = min(BM, p.m - m0);
   const int i0 = zr * kchunk;
   const int i1 = min(p.k >> 7, i0 + kchunk);
@@ -658,7 +666,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 
   // lane holds C[m0 + mt*16 + 4kg + e][n0 + ns*16 + ln]
-  const bool split = gridDim.x > 1;
+  const bool split = ks > 1;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -1284,8 +1292,14 @@ int launch_w4a16_tile(const W4Params& p, const W4Plan& pl, float* part, hipStrea
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((w4a16_tile_kernel<T, MT, NS, PF>), dim3((unsigned)pl.ks, (unsigned)pl.n_tiles, (unsigned)pl.m_blocks),
-                     dim3(256), pl.lds, stream, p, part, pl.kchunk);
+  const int64_t pairs = (int64_t)pl.ks * pl.n_tiles;
+  const int64_t grid = (pairs + 7) / 8 * 8 * pl.m_blocks;
+  if (grid > 0x7fffffff) {
+    ss_host::set_error("w4a16 gemm: %lld tiled workgroups", (long long)grid);
+    return SS_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL((w4a16_tile_kernel<T, MT, NS, PF>), dim3((unsigned)grid), dim3(256), pl.lds, stream, p, part,
+                     pl.kchunk, pl.ks, pl.n_tiles, pl.m_blocks);
   int st = ss_host::launch_status("w4a16 gemm (tiled)");
   if (st != SS_OK || pl.ks == 1) return st;
   const bool vec = p.n % 4 == 0;
