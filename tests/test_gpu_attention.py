@@ -461,6 +461,26 @@ def test_varlen_full_mixed_step_every_row(device):
     assert_attn_close(out, np.concatenate(ref, axis=0), "C3 every row")
 
 
+def test_long_contexts_decode_and_prefill(device):
+    """Lengths far past the bench's (C2 clips at 8192): one decode over 131072 keys (8192
+    blocks, 4096 pairs, a table row of 8192 entries), one over 70001, a 1024-token chunk
+    behind a 20000-token prior and two one-key sequences, in one packed call; every row
+    against the float64 oracle."""
+    print("long contexts: ctx [131072, 1, 70001, 21024, 5]", flush=True)
+    ctx, ql = [131072, 1, 70001, 21024, 5], [1, 1, 1, 1024, 1]
+    b = workloads.build_batch(ctx, ql, n_q=8, n_kv=2, head_dim=64, block_size=16, dtype=torch.bfloat16,
+                              device=device, seed=21)
+    assert b.block_tables.shape[1] == 8192
+    out = paged_attention_varlen(b.q, b.kv_cache, b.block_tables, b.cu_seqlens, b.context_lens, 0, b.scale,
+                                 16, b.max_query_len)
+    torch.cuda.synchronize()
+    cu = b.cu_seqlens.cpu().tolist()
+    q = f64(b.q)
+    queries = [q[cu[i]:cu[i + 1]].transpose(1, 0, 2) for i in range(b.batch)]
+    ref = oracle_paged_rows(b.kv_cache, b.tables_host, b.ctx_host, queries, b.scale, 16)
+    assert_attn_close(out, np.concatenate(ref, axis=0), "long contexts")
+
+
 @pytest.mark.parametrize("max_q", [0, 1, 20, 40])
 def test_varlen_query_longer_than_max_query_len_is_zeroed_and_flagged(device, max_q):
     """A packed sequence longer than max_query_len (a broken caller promise): the rows

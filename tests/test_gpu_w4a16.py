@@ -114,23 +114,42 @@ def test_batch1_gemv_strided_activation(device):
     _assert_close(y, ref, "gemv strided x")
 
 
+# (plans as the host computes them for 256 CUs: ranges x stages, weight tiles, M blocks)
 @pytest.mark.parametrize("m,k,n,g,act,sdt", [
-    (50, 3584, 12750, 128, torch.bfloat16, torch.float16),   # 4 K ranges of 8, 8, 8, 4 stages; ragged M, N
-    (33, 3584, 2000, 896, torch.float16, torch.bfloat16),    # groups of 7 stages straddle the ranges
+    (50, 3072, 12750, 128, torch.bfloat16, torch.float16),   # 3 ranges of 8 stages; 100 tiles: 300 pairs, 4 padding ids
+    (33, 3584, 2000, 896, torch.float16, torch.bfloat16),    # 7 ranges of 4 stages: groups of 7 stages straddle them
     (100, 4096, 1000, 256, torch.bfloat16, torch.float32),   # 64x64 wave tiles, a partial second M block
+    (130, 1792, 700, 128, torch.bfloat16, torch.float16),    # 3 M blocks of one weight tile on one XCD; 21 pairs
     (24, 8192, 3000, 512, torch.float16, torch.float16),     # 32-row activation tiles
-    (9, 8192, 700, 128, torch.bfloat16, torch.bfloat16),     # m <= 16 at K >= 8192 takes the tiled kernel
-    (16, 1024, 24600, 128, torch.bfloat16, torch.float16),   # m <= 16 at N >= 24576 takes it too
+    (9, 8192, 700, 256, torch.bfloat16, torch.bfloat16),     # m <= 16, g 256 (the skinny kernel takes only g 128)
+    (16, 1024, 24600, 256, torch.bfloat16, torch.float16),   # m <= 16 at N >= 24576, unsplit, 193 tiles
 ])
 def test_tiled_split_k(device, m, k, n, g, act, sdt):
     """The tiled kernel (activations shared through LDS, K split over workgroups with
-    fp32 partials added in range order): uneven ranges, groups straddling ranges,
-    ragged M and N, every scale dtype."""
+    fp32 partials added in range order): groups straddling ranges, ragged M and N, the
+    XCD-grouped grid with padding ids, every scale dtype."""
     x, qw, s, z, ref = _host_case(n, k, m, g, seed=m + k + n, act=act, sdt=sdt, zeros="random")
     xd, qd, sd, zd = x.to(device), qw.to(device), s.to(device), z.to(device)
     y = w4a16_gemm(xd, qd, sd, zd, g)
     _assert_close(y, ref, f"tiled m={m} k={k} n={n} g={g}")
     assert torch.equal(y, w4a16_gemm(xd, qd, sd, zd, g))  # repeat: bit-identical
+
+
+def test_tiled_uneven_ranges_from_the_table_cap(device):
+    """K = 15360 at M = 40 over 258 weight tiles: one range per tile would need a 122 KB
+    scale table, so the host splits K until a range's table fits 40 KB -- 4 ranges of 32,
+    32, 32 and 24 stages (the only way ranges come out uneven). Every column against the
+    fp32 dequant-then-matmul on the device, 64 against the float64 oracle."""
+    k, n, m = 15360, 33000, 40
+    lin = workloads.w4a16_linear(k, n, m, device=device, seed=5)
+    y = w4a16_gemm(lin.x, lin.qweight, lin.scales, lin.qzeros, lin.group_size)
+    torch.cuda.synchronize()
+    _assert_close(y, workloads.w4a16_reference_fp32(lin).double().cpu().numpy(), "uneven ranges vs fp32 torch")
+    cols = np.random.default_rng(5).choice(n, 64, replace=False)
+    ref = quant.w4a16_gemm(lin.x.double().cpu().numpy(), lin.qweight[cols].cpu().numpy(),
+                           lin.scales[cols].double().cpu().numpy(), lin.qzeros[cols].cpu().numpy(), lin.group_size)
+    _assert_close(y[:, cols], ref, "uneven ranges vs oracle")
+    assert torch.equal(y, w4a16_gemm(lin.x, lin.qweight, lin.scales, lin.qzeros, lin.group_size))
 
 
 def test_tiled_without_workspace_takes_untiled_kernel(device):
