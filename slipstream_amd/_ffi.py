@@ -126,6 +126,18 @@ def i64_array(values) -> ctypes.Array:
     return (ctypes.c_int64 * len(vals))(*vals)
 
 
+_I64x2 = ctypes.c_int64 * 2
+_I64x3 = ctypes.c_int64 * 3
+
+
+def i64x2(a: int, b: int) -> ctypes.Array:
+    return _I64x2(a, b)
+
+
+def i64x3(a: int, b: int, c: int) -> ctypes.Array:
+    return _I64x3(a, b, c)
+
+
 def check(status: int, what: str) -> None:
     """Map a C status to the reference's exception classes."""
     if status == SS_OK:
@@ -139,8 +151,16 @@ def check(status: int, what: str) -> None:
     raise KernelError(msg)
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device: torch.device) -> int:
-    """Raw ``hipStream_t`` of torch's current stream on ``device``."""
+    """Raw ``hipStream_t`` of torch's current stream on ``device`` (torch's own raw
+    accessor when it has one: a tenth of the cost of building the stream object, which
+    matters for the microsecond-scale launches of a decode step)."""
+    if _raw_stream is not None:
+        idx = device.index
+        return _raw_stream(torch.cuda.current_device() if idx is None else idx)
     return int(torch.cuda.current_stream(device).cuda_stream)
 
 

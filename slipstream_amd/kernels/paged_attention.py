@@ -24,7 +24,7 @@ import os
 import torch
 
 from slipstream_amd import _ffi
-from slipstream_amd.kernels._common import require_device, unit_last_stride
+from slipstream_amd.kernels._common import cache_planes, require_device, unit_last_stride
 
 _SUPPORTED = (torch.bfloat16, torch.float16)
 _WS_BYTES: dict[tuple, int] = {}
@@ -37,7 +37,8 @@ def _debug() -> bool:
 
 def _strides(x: torch.Tensor, dims: tuple[int, ...]) -> list[int]:
     """Element strides of ``dims``; a size-1 dim is never indexed, so it reports 0."""
-    return [x.stride(d) if x.shape[d] > 1 else 0 for d in dims]
+    st, sh = x.stride(), x.shape
+    return [st[d] if sh[d] > 1 else 0 for d in dims]
 
 
 def _check_cache(kv_cache: torch.Tensor, layer_idx: int, block_size: int, head_dim: int) -> None:
@@ -108,18 +109,15 @@ def paged_attention(
     q = unit_last_stride(q)
     block_tables = _int32(block_tables)
     seq_lens = _int32(seq_lens.reshape(-1))
-    kc = kv_cache[layer_idx, 0]
-    vc = kv_cache[layer_idx, 1]
-    if kc.stride(3) != 1 or kc.data_ptr() % 16 or vc.data_ptr() % 16:
-        raise _ffi.KernelError("kv_cache planes must have unit head_dim stride and 16-byte alignment")
+    k_ptr, v_ptr, c_str = cache_planes(kv_cache, layer_idx, "paged_attention")
     out = torch.empty((batch, tq, n_q, head_dim), device=q.device, dtype=q.dtype)
     code = _ffi.dtype_code(q.dtype)
     ws = _workspace(q.device, batch, n_q, n_kv, head_dim, tq, code)
     status = _ffi.lib().ss_paged_attention(
         q.data_ptr(),
         out.data_ptr(),
-        kc.data_ptr(),
-        vc.data_ptr(),
+        k_ptr,
+        v_ptr,
         block_tables.data_ptr(),
         seq_lens.data_ptr(),
         batch,
@@ -130,9 +128,9 @@ def paged_attention(
         block_tables.shape[1],
         block_size,
         kv_cache.shape[2],
-        _ffi.i64_array(_strides(q, (0, 1, 2))),
-        _ffi.i64_array(_strides(out, (0, 1, 2))),
-        _ffi.i64_array([kc.stride(0), kc.stride(1), kc.stride(2)]),
+        _ffi.i64x3(*_strides(q, (0, 1, 2))),
+        _ffi.i64x3(*_strides(out, (0, 1, 2))),
+        _ffi.i64x3(*c_str),
         block_tables.stride(0),
         float(scale),
         code,
@@ -211,10 +209,7 @@ def paged_attention_shared_prefix(
             raise ValueError("block_tables rows differ inside the shared prefix")
         if int(seq_lens.min()) < prefix_blocks * block_size:
             raise ValueError("a sequence is shorter than the shared prefix")
-    kc = kv_cache[layer_idx, 0]
-    vc = kv_cache[layer_idx, 1]
-    if kc.stride(3) != 1 or kc.data_ptr() % 16 or vc.data_ptr() % 16:
-        raise _ffi.KernelError("kv_cache planes must have unit head_dim stride and 16-byte alignment")
+    k_ptr, v_ptr, c_str = cache_planes(kv_cache, layer_idx, "paged_attention_shared_prefix")
     out = torch.empty((batch, 1, n_q, head_dim), device=q.device, dtype=q.dtype)
     code = _ffi.dtype_code(q.dtype)
     key = (q.device.index, batch, n_q, n_kv, head_dim, block_size, prefix_blocks, code)
@@ -232,8 +227,8 @@ def paged_attention_shared_prefix(
     status = _ffi.lib().ss_paged_attention_shared_prefix(
         q.data_ptr(),
         out.data_ptr(),
-        kc.data_ptr(),
-        vc.data_ptr(),
+        k_ptr,
+        v_ptr,
         block_tables.data_ptr(),
         seq_lens.data_ptr(),
         batch,
@@ -244,9 +239,9 @@ def paged_attention_shared_prefix(
         block_size,
         kv_cache.shape[2],
         prefix_blocks,
-        _ffi.i64_array(_strides(q, (0, 1))),
-        _ffi.i64_array(_strides(out, (0, 2))),
-        _ffi.i64_array([kc.stride(0), kc.stride(1), kc.stride(2)]),
+        _ffi.i64x2(*_strides(q, (0, 1))),
+        _ffi.i64x2(*_strides(out, (0, 2))),
+        _ffi.i64x3(*c_str),
         block_tables.stride(0),
         float(scale),
         code,
@@ -372,17 +367,14 @@ def paged_attention_varlen(
     ctx = _int32(context_lens.reshape(-1))
     if _debug():
         _check_stream(cu, total, max_query_len)
-    kc = kv_cache[layer_idx, 0]
-    vc = kv_cache[layer_idx, 1]
-    if kc.stride(3) != 1 or kc.data_ptr() % 16 or vc.data_ptr() % 16:
-        raise _ffi.KernelError("kv_cache planes must have unit head_dim stride and 16-byte alignment")
+    k_ptr, v_ptr, c_str = cache_planes(kv_cache, layer_idx, "paged_attention_varlen")
     code = _ffi.dtype_code(q.dtype)
     ws = _workspace(q.device, batch, n_q, n_kv, head_dim, max(1, max_query_len), code)
     status = _ffi.lib().ss_paged_attention_varlen(
         q.data_ptr(),
         out.data_ptr(),
-        kc.data_ptr(),
-        vc.data_ptr(),
+        k_ptr,
+        v_ptr,
         block_tables.data_ptr(),
         cu.data_ptr(),
         ctx.data_ptr(),
@@ -395,9 +387,9 @@ def paged_attention_varlen(
         block_tables.shape[1],
         block_size,
         kv_cache.shape[2],
-        _ffi.i64_array(_strides(q, (0, 1))),
-        _ffi.i64_array(_strides(out, (0, 1))),
-        _ffi.i64_array([kc.stride(0), kc.stride(1), kc.stride(2)]),
+        _ffi.i64x2(*_strides(q, (0, 1))),
+        _ffi.i64x2(*_strides(out, (0, 1))),
+        _ffi.i64x3(*c_str),
         block_tables.stride(0),
         float(scale),
         code,

@@ -13,7 +13,7 @@ from __future__ import annotations
 import torch
 
 from slipstream_amd import _ffi
-from slipstream_amd.kernels._common import require_device
+from slipstream_amd.kernels._common import cache_planes, require_device
 
 
 def _token_view(x: torch.Tensor) -> tuple[int, int, list[int], torch.Tensor]:
@@ -73,15 +73,14 @@ def reshape_and_cache(
 
     n_outer, n_inner, k_str, k = _token_view(k)
     _, _, v_str, v = _token_view(v)
-    kc = kv_cache[layer_idx, 0]
-    vc = kv_cache[layer_idx, 1]
+    k_ptr, v_ptr, c_str = cache_planes(kv_cache, layer_idx, "reshape_and_cache", aligned=False)
     num_slots = kv_cache.shape[2] * block_size
     lib = _ffi.lib()
     status = lib.ss_reshape_and_cache(
         k.data_ptr(),
         v.data_ptr(),
-        kc.data_ptr(),
-        vc.data_ptr(),
+        k_ptr,
+        v_ptr,
         slot_mapping.data_ptr(),
         n_outer,
         n_inner,
@@ -89,9 +88,9 @@ def reshape_and_cache(
         head_dim,
         block_size,
         num_slots,
-        _ffi.i64_array(k_str),
-        _ffi.i64_array(v_str),
-        _ffi.i64_array([kc.stride(0), kc.stride(1), kc.stride(2)]),
+        _ffi.i64x3(*k_str),
+        _ffi.i64x3(*v_str),
+        _ffi.i64x3(*c_str),
         kv_cache.element_size(),
         _ffi.stream_ptr(kv_cache.device),
     )

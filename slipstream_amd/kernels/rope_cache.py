@@ -14,7 +14,7 @@ from __future__ import annotations
 import torch
 
 from slipstream_amd import _ffi
-from slipstream_amd.kernels._common import require_device
+from slipstream_amd.kernels._common import cache_planes, require_device
 
 
 def _token_layout(x: torch.Tensor, unsqueeze_dim: int) -> tuple[int, int, list[int]]:
@@ -107,15 +107,15 @@ def rope_and_cache(
         slot_mapping = slot_mapping.to(torch.int64)
     slot_mapping = slot_mapping.reshape(-1).contiguous()
     _, _, o_str = _token_layout(out, unsqueeze_dim)
-    kc, vc = kv_cache[layer_idx, 0], kv_cache[layer_idx, 1]
+    k_ptr, v_ptr, c_str = cache_planes(kv_cache, layer_idx, "rope_and_cache", aligned=False)
     lib = _ffi.lib()
     status = lib.ss_rope_and_cache(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(), sin.data_ptr(), out.data_ptr(),
-        kc.data_ptr(), vc.data_ptr(), slot_mapping.data_ptr(), n_outer, n_inner, n_q, n_kv, head_dim,
+        k_ptr, v_ptr, slot_mapping.data_ptr(), n_outer, n_inner, n_q, n_kv, head_dim,
         block_size, kv_cache.shape[2] * block_size,
         _ffi.i64_array(q_str), _ffi.i64_array(k_str), _ffi.i64_array(v_str), _ffi.i64_array(o_str),
         _ffi.i64_array(_cs_strides(cos, q)), _ffi.i64_array(_cs_strides(sin, q)),
-        _ffi.i64_array([kc.stride(0), kc.stride(1), kc.stride(2)]),
+        _ffi.i64x3(*c_str),
         _ffi.dtype_code(q.dtype), _ffi.stream_ptr(q.device),
     )
     _ffi.check(status, "rope_and_cache")
