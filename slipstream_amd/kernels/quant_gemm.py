@@ -23,6 +23,9 @@ from slipstream_amd.kernels._common import require_device
 # Split-K partials of the tiled kernel, one buffer per (device, stream): every call writes
 # the partials it reads, so the buffer needs no initialisation and keeps no state.
 _WORKSPACE: dict[tuple[int, int], torch.Tensor] = {}
+# Workspace bytes the library asks for, by shape (a plan depends on the shape and the
+# device's CU count only).
+_WS_NEED: dict[tuple, int] = {}
 
 
 def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
@@ -80,11 +83,17 @@ def w4a16_gemm(
     act = _ffi.dtype_code(x.dtype)
     sdt = _ffi.dtype_code(scales.dtype)
     lib = _ffi.lib()
-    need = _ffi.ctypes.c_int64(0)
-    _ffi.check(lib.ss_w4a16_workspace_size(m, out_features, in_features, group_size, act, _ffi.ctypes.byref(need)),
-               "w4a16 workspace")
+    key = (x.device.index, m, out_features, in_features, group_size, act)
+    need = _WS_NEED.get(key)
+    if need is None:
+        out_b = _ffi.ctypes.c_int64(0)
+        _ffi.check(lib.ss_w4a16_workspace_size(m, out_features, in_features, group_size, act,
+                                               _ffi.ctypes.byref(out_b)), "w4a16 workspace")
+        if len(_WS_NEED) > 4096:  # many distinct shapes: start over
+            _WS_NEED.clear()
+        need = _WS_NEED[key] = int(out_b.value)
     stream = _ffi.stream_ptr(x.device)
-    ws = _workspace(x.device, stream, int(need.value))
+    ws = _workspace(x.device, stream, need)
     o2 = out.view(m, out_features)
     status = lib.ss_w4a16_gemm(
         x2.data_ptr(),
