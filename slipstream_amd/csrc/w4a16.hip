@@ -1075,10 +1075,178 @@ __global__ __launch_bounds__(512) void w4a16_gemv_kernel(const W4Params p) {
   }
 }
 
+// Narrow kernel (1 <= m <= 4, g == 128): the small-batch GEMV with its dot products on
+// MFMA 16x16x32 instead of v_dot2, which leaves the VALU only the nibble unpack (seven
+// instructions per 32-bit word) and two FMAs per activation row and load.
+//
+// A workgroup owns 4 J weight rows; its waves split K into slices of W 512-key windows.
+// One weight load instruction moves 4 rows x 256 contiguous bytes (one window of each):
+// MFMA B column c is row c >> 2, piece c & 3 (128 keys = one group) of the window, and
+// the four lanes of a column (k-blocks kg) hold 32 consecutive keys of it, one 32-bit
+// word per MFMA. A row a holds activation row a & 3 over piece a >> 2. Product entry
+// (a, c) is a dot product of the same keys only where the pieces agree (a >> 2 == c & 3):
+// lane 16 (c & 3) + c holds those entries of column c, element i = activation row i, as
+// G = sum over the group of x (MAGIC + q). The same A against an all-ones B gives X =
+// sum x of (row, piece) in the same lanes and elements, so the fold s G - s (MAGIC + z) X
+// applies to the MFMA outputs directly. The other entries are computed and dropped (the
+// matrix unit has the cycles: 4 MFMAs per 2048 weights).
+//
+// Each wave stages its own activation slice in its own LDS rows (permuted to the nibble
+// order; its LDS operations run in order, so no barrier), the weights stream straight
+// into registers (all J W loads issued up front, consumed in order as they land), and
+// the waves' slices and the four pieces of each row add in LDS in a fixed order.
+// SD: the scale dtype.
+//
+// LDS: x [waves][MR][512 W] permuted | partials [waves][4 J rows][MR][4 pieces] floats |
+//      (scale, MAGIC + zero) [waves][4 J rows][4 W groups] float pairs
+template <int SD>
+__device__ __forceinline__ float narrow_scale(uint32_t bits) {
+  if constexpr (SD == SS_DTYPE_F16) return (float)__builtin_bit_cast(f16_t, (uint16_t)(bits & 0xFFFFu));
+  if constexpr (SD == SS_DTYPE_BF16) return __builtin_bit_cast(float, bits << 16);
+  return __builtin_bit_cast(float, bits);
+}
+
+template <typename T, int MR, int J, int W, int SD>
+__global__ __launch_bounds__(512) void w4a16_narrow_kernel(const W4Params p) {
+  typedef W4Elem<T> E;
+  extern __shared__ __attribute__((aligned(16))) char s_dyn[];
+  constexpr int SL = 512 * W;  // keys of a wave's slice
+  constexpr int IT = J * W;    // weight loads per lane
+  const int K = p.k;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const int n0 = blockIdx.x * 4 * J;
+  const int c = lane & 15, kg = lane >> 4;
+  const int cr = c >> 2, cp = c & 3;  // column c: row cr of a four-row load, piece cp of the window
+  const int k0 = wave * SL;
+  T* const s_xw = (T*)s_dyn + (size_t)wave * MR * SL;
+  float* const s_part = (float*)(s_dyn + (size_t)nw * MR * SL * sizeof(T));
+  // the wave's (scale, MAGIC + zero) pairs [4 J rows][4 W groups], after the partials
+  float2* const s_sz = (float2*)(s_part + (size_t)nw * 4 * J * MR * 4) + (size_t)wave * 16 * J * W;
+  // Loads in the order they are consumed (the vector-memory counter retires in order):
+  // the activation slice, the scales and zero points, then the weights.
+  // Activation rows at or past m read as zero: their offsets start past the
+  // descriptor's end since x_stride >= K.
+  const __amdgpu_buffer_rsrc_t rx =
+      buffer_rsrc(p.x, (uint32_t)(((int64_t)(p.m - 1) * p.x_stride + K) * sizeof(T)));
+  u32x4 xin[MR * W];
+#pragma unroll
+  for (int e2 = 0; e2 < MR * W; ++e2) {
+    const int q = lane + 64 * e2;
+    const int r = q / (64 * W), c8 = q - r * (64 * W);
+    xin[e2] = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)((r * p.x_stride + k0 + 8 * c8) * sizeof(T)), 0, 0));
+  }
+  // The (scale, zero) block of the wave's rows and groups: lane (row lr, part lh) reads
+  // IT / 4 consecutive groups of its row (rows past N read as zero, past the
+  // descriptors' ends); decoded once into LDS below.
+  static_assert(IT == 8 || IT == 16, "two or four groups per lane in the scale block");
+  static_assert(SD >= 0, "a fixed scale dtype");
+  constexpr int esize = SD == SS_DTYPE_F32 ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.sc, (uint32_t)((int64_t)p.n * p.groups * esize));
+  const __amdgpu_buffer_rsrc_t rzp = buffer_rsrc(p.qz, (uint32_t)((int64_t)p.n * p.groups * 4));
+  constexpr int LPR = 16 / J;  // lanes per row
+  const int lr = lane / LPR, lh = lane - lr * LPR;
+  const int gq = (n0 + lr) * p.groups + k0 / 128 + lh * (IT / 4);
+  u32x4 zq = {0u, 0u, 0u, 0u}, sq = {0u, 0u, 0u, 0u};
+  if constexpr (IT == 16) {
+    zq = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rzp, gq * 4, 0, 0));
+    if constexpr (esize == 4) {
+      sq = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsc, gq * 4, 0, 0));
+    } else {
+      const u32x2 t = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rsc, gq * 2, 0, 0));
+      sq = u32x4{t[0] & 0xFFFFu, t[0] >> 16, t[1] & 0xFFFFu, t[1] >> 16};
+    }
+  } else {
+    const u32x2 z2 = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rzp, gq * 4, 0, 0));
+    zq = u32x4{z2[0], z2[1], 0u, 0u};
+    if constexpr (esize == 4) {
+      const u32x2 t = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rsc, gq * 4, 0, 0));
+      sq = u32x4{t[0], t[1], 0u, 0u};
+    } else {
+      const uint32_t t = __builtin_amdgcn_raw_buffer_load_b32(rsc, gq * 2, 0, 0);
+      sq = u32x4{t & 0xFFFFu, t >> 16, 0u, 0u};
+    }
+  }
+  // one descriptor over the workgroup's rows (rows past N read as zero)
+  const int live_rows = min(4 * J, p.n - n0);
+  const __amdgpu_buffer_rsrc_t rw =
+      buffer_rsrc(p.qw + (int64_t)n0 * (K / 8), (uint32_t)live_rows * (uint32_t)(K / 2));
+  const int vrow = cr * (K / 2) + k0 / 2 + 64 * cp + 16 * kg;
+  u32x4 wv[IT];
+#pragma unroll
+  for (int u = 0; u < IT; ++u) {
+    const int w = u / J, j = u - w * J;
+    wv[u] = __builtin_bit_cast(u32x4,
+                               __builtin_amdgcn_raw_buffer_load_b128(rw, vrow, j * 2 * K + 256 * w, kNonTemporal));
+  }
+
+  // the wave's activation slice -> its LDS rows, permuted to the nibble order
+#pragma unroll
+  for (int e2 = 0; e2 < MR * W; ++e2) {
+    const int q = lane + 64 * e2;
+    const int r = q / (64 * W), c8 = q - r * (64 * W);
+    store16(s_xw + r * SL + 8 * c8, permute_x(xin[e2]));
+  }
+#pragma unroll
+  for (int e = 0; e < IT / 4; ++e)
+    s_sz[lr * 4 * W + lh * (IT / 4) + e] = make_float2(narrow_scale<SD>(sq[e]), E::kMagic + (float)(int)zq[e]);
+  __builtin_amdgcn_wave_barrier();
+
+  const uint32_t magic = in_vgpr(E::kMagicPair);
+  const uint32_t one2 = in_vgpr(E::kOnePair);
+  const u32x4 ones = {one2, one2, one2, one2};
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  // A row c of this lane: activation row c & 3 (a duplicate where m has fewer rows)
+  const int xr = MR == 1 ? 0 : (MR == 2 ? (cp & 1) : cp);
+  f32x4 tot[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) tot[j] = zero4;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    u32x4 a[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) a[s] = load16(s_xw + xr * SL + 512 * w + 128 * cr + 32 * kg + 8 * s);
+    f32x4 X = Elem<T>::mfma(a[0], ones, zero4);
+#pragma unroll
+    for (int s = 1; s < 4; ++s) X = Elem<T>::mfma(a[s], ones, X);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int u = w * J + j;
+      f32x4 G = Elem<T>::mfma(a[0], nibbles_to_operand(wv[u][0], magic), zero4);
+#pragma unroll
+      for (int s = 1; s < 4; ++s) G = Elem<T>::mfma(a[s], nibbles_to_operand(wv[u][s], magic), G);
+      const float2 sz = s_sz[(4 * j + cr) * 4 * W + 4 * w + cp];
+#pragma unroll
+      for (int i = 0; i < MR; ++i) tot[j][i] = fmaf(sz.x, fmaf(-sz.y, X[i], G[i]), tot[j][i]);
+    }
+  }
+
+  // lanes with kg == cp hold row 4 j + cr, piece cp; add pieces and waves in order
+  if (kg == cp) {
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int i = 0; i < MR; ++i) s_part[((wave * 4 * J + 4 * j + cr) * MR + i) * 4 + cp] = tot[j][i];
+  }
+  __syncthreads();
+  if (threadIdx.x < 4 * J * MR) {
+    const int rr = threadIdx.x / MR, i = threadIdx.x - rr * MR;
+    float y = 0.f;
+    for (int w2 = 0; w2 < nw; ++w2) {
+      const float* q = s_part + ((w2 * 4 * J + rr) * MR + i) * 4;
+      y += (q[0] + q[1]) + (q[2] + q[3]);
+    }
+    if (i < p.m && n0 + rr < p.n) ((T*)p.out)[(int64_t)i * p.o_stride + n0 + rr] = (T)y;
+  }
+}
+
 struct W4Plan {
   bool fast;
   bool wide;
   bool xlds;
+  int narrow;  // activation rows of the narrow kernel (1, 2 or 4), 0: not used
   int gemv;  // 1: the batch-1 GEMV kernel
   bool tile;  // the tiled kernel (activations shared through LDS)
   bool skinny;  // the skinny kernel (m <= 64, K split over the waves of one workgroup)
@@ -1219,6 +1387,15 @@ W4Plan plan_w4a16(int64_t m, int64_t n, int64_t k, int g, bool act16, bool allow
   // the LDS budget. (A second activation row makes the compiler hoist every
   // activation read and spill: m >= 2 takes the MFMA kernel.)
   const int gemv_slice = k <= 8192 ? 1024 : 2048;
+  if (m <= 4 && g == 128 && k % gemv_slice == 0 && k <= 16384) {
+    const int mr = m == 1 ? 1 : (m == 2 ? 2 : 4);
+    const int64_t waves = k / gemv_slice;
+    pl.narrow = mr;
+    // x slices | partials | (scale, zero) pairs of 16 rows x slice / 128 groups
+    pl.lds = (size_t)waves * mr * gemv_slice * 2 + (size_t)waves * 16 * mr * 4 * 4 + (size_t)waves * 16 * (gemv_slice / 128) * 8;
+    pl.n_tiles = (int)((n + 15) / 16);
+    return pl;
+  }
   if (m == 1 && k % gemv_slice == 0 && k <= 16384) {
     const int mr = 1;
     const size_t lds = (size_t)mr * k * 2 + (size_t)(k / 32) * mr * 4 + (size_t)(k / gemv_slice) * 16 * mr * 4;
@@ -1370,8 +1547,43 @@ int launch_w4a16_skinny_mt(const W4Params& p, const W4Plan& pl, hipStream_t stre
   return SS_ERR_UNSUPPORTED;
 }
 
+// at most 8 waves of 2048 keys and 4 activation rows
+constexpr int kNarrowLdsMax = 160 * 1024;
+
+template <typename T, int MR, int J, int W, int SD>
+int launch_w4a16_narrow(const W4Params& p, const W4Plan& pl, hipStream_t stream) {
+  static bool attr_set = false;  // per instantiation; the attribute is process-wide
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)w4a16_narrow_kernel<T, MR, J, W, SD>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kNarrowLdsMax) != hipSuccess) {
+      ss_host::set_error("w4a16 gemm: cannot reserve %d bytes of LDS", kNarrowLdsMax);
+      return SS_ERR_UNSUPPORTED;
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((w4a16_narrow_kernel<T, MR, J, W, SD>), dim3((unsigned)pl.n_tiles),
+                     dim3((unsigned)(64 * (p.k / (512 * W)))), pl.lds, stream, p);
+  return ss_host::launch_status("w4a16 gemm (narrow)");
+}
+
+template <typename T, int MR, int SD>
+int launch_w4a16_narrow_sd(const W4Params& p, const W4Plan& pl, hipStream_t stream) {
+  if (p.k <= 8192) return launch_w4a16_narrow<T, MR, 4, 2, SD>(p, pl, stream);
+  return launch_w4a16_narrow<T, MR, 4, 4, SD>(p, pl, stream);
+}
+
+template <typename T, int MR>
+int launch_w4a16_narrow_mr(const W4Params& p, const W4Plan& pl, hipStream_t stream) {
+  if (p.sdt == SS_DTYPE_F16) return launch_w4a16_narrow_sd<T, MR, SS_DTYPE_F16>(p, pl, stream);
+  if (p.sdt == SS_DTYPE_BF16) return launch_w4a16_narrow_sd<T, MR, SS_DTYPE_BF16>(p, pl, stream);
+  return launch_w4a16_narrow_sd<T, MR, SS_DTYPE_F32>(p, pl, stream);
+}
+
 template <typename T>
 int launch_w4a16_typed(const W4Params& p, const W4Plan& pl, float* part, hipStream_t stream) {
+  if (pl.narrow == 1) return launch_w4a16_narrow_mr<T, 1>(p, pl, stream);
+  if (pl.narrow == 2) return launch_w4a16_narrow_mr<T, 2>(p, pl, stream);
+  if (pl.narrow == 4) return launch_w4a16_narrow_mr<T, 4>(p, pl, stream);
   if (pl.skinny) return launch_w4a16_skinny_mt<T, 1>(p, pl, stream);
   if (pl.tile) {
     if (pl.mt == 1) return launch_w4a16_tile<T, 1, 2, 8>(p, pl, part, stream);

@@ -96,13 +96,40 @@ def test_activation_paths(device, m, k, g):
     (40, 16384, 64, torch.float16, torch.bfloat16),     # the largest K the GEMV takes
 ])
 def test_batch1_gemv(device, n, k, g, act, sdt):
-    """M = 1 takes the bandwidth GEMV (one 1024-key wave slice per wave up to K = 8192,
-    2048-key slices up to 16384; four lanes per row): random zero points, every scale
-    dtype, ragged N."""
+    """M = 1: g = 128 takes the narrow MFMA kernel, g = 32 / 64 the bandwidth GEMV (one
+    1024-key wave slice per wave up to K = 8192, 2048-key slices up to 16384): random zero
+    points, every scale dtype, ragged N."""
     x, qw, s, z, ref = _host_case(n, k, 1, g, seed=n + k + g, act=act, sdt=sdt, zeros="random")
     y = w4a16_gemm(x.to(device), qw.to(device), s.to(device), z.to(device), g)
     assert y.shape == (1, n) and y.dtype == act
     _assert_close(y, ref, f"gemv n={n} k={k} g={g}")
+
+
+@pytest.mark.parametrize("m,n,k,act,sdt", [
+    (1, 100, 1024, torch.bfloat16, torch.float16),    # one wave; N not a multiple of 16
+    (2, 333, 4096, torch.float16, torch.bfloat16),
+    (3, 40, 8192, torch.bfloat16, torch.float32),     # 8 waves of 1024 keys; row 3 of the A tile is empty
+    (4, 17, 14336, torch.float16, torch.float16),     # 7 waves of 2048 keys (the down projection)
+    (4, 64, 16384, torch.bfloat16, torch.bfloat16),   # the largest K it takes
+    (2, 4100, 2048, torch.bfloat16, torch.float16),   # many workgroups, a partial last one
+])
+def test_narrow_mfma_kernel(device, m, n, k, act, sdt):
+    """1 <= M <= 4 with g = 128 takes the narrow kernel (dot products on MFMA, four-row
+    weight loads, A rows = (piece, activation row)): random zero points, every scale and
+    activation dtype, ragged N."""
+    x, qw, s, z, ref = _host_case(n, k, m, 128, seed=n + k + m, act=act, sdt=sdt, zeros="random")
+    y = w4a16_gemm(x.to(device), qw.to(device), s.to(device), z.to(device), 128)
+    assert y.shape == (m, n) and y.dtype == act
+    _assert_close(y, ref, f"narrow m={m} n={n} k={k}")
+
+
+def test_narrow_strided_activation(device):
+    """Three strided activation rows (views into a wider buffer) through the narrow kernel."""
+    x, qw, s, z, ref = _host_case(96, 4096, 3, 128, seed=78, zeros="random")
+    xd = torch.zeros((5, 8192), dtype=x.dtype, device=device)[1:4, 2048:6144]
+    xd.copy_(x.to(device))
+    y = w4a16_gemm(xd, qw.to(device), s.to(device), z.to(device), 128)
+    _assert_close(y, ref, "narrow strided x")
 
 
 def test_batch1_gemv_strided_activation(device):
