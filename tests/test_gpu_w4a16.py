@@ -133,11 +133,11 @@ def test_narrow_strided_activation(device):
 
 
 def test_batch1_gemv_strided_activation(device):
-    """A strided single activation row (a view into a wider buffer) through the GEMV."""
-    x, qw, s, z, ref = _host_case(96, 4096, 1, 128, seed=77, zeros="random")
+    """A strided single activation row (a view into a wider buffer) through the GEMV (g = 64)."""
+    x, qw, s, z, ref = _host_case(96, 4096, 1, 64, seed=77, zeros="random")
     xd = torch.zeros((3, 8192), dtype=x.dtype, device=device)[1:2, 1024:5120]
     xd.copy_(x.to(device))
-    y = w4a16_gemm(xd, qw.to(device), s.to(device), z.to(device), 128)
+    y = w4a16_gemm(xd, qw.to(device), s.to(device), z.to(device), 64)
     _assert_close(y, ref, "gemv strided x")
 
 
