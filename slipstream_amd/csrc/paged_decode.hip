@@ -331,8 +331,13 @@ __device__ __forceinline__ void load_pair_scalar(const AttnParams& p, const Scal
     int vt = c.kvt - (bi << p.bs_shift);  // valid tokens of the block
     vt = vt < 0 ? 0 : (vt > p.block_size ? p.block_size : vt);
     const int live = vt > tib ? vt - tib : 0;
-    const int64_t off = ok ? (int64_t)ph[x] * c.blk_bytes + (int64_t)tib * c.tok_bytes : 0;
-    const int bytes = ok ? live * c.tok_bytes : 0;
+    // offset and size through readfirstlane: they are uniform, but where the compiler
+    // cannot prove it (a select on a lane mask) it wraps every load of the tile in a
+    // waterfall loop over the descriptor
+    int64_t off = ok ? (int64_t)ph[x] * c.blk_bytes + (int64_t)tib * c.tok_bytes : 0;
+    off = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(off >> 32)) << 32) |
+                    (uint32_t)__builtin_amdgcn_readfirstlane((int)off));
+    const int bytes = __builtin_amdgcn_readfirstlane(ok ? live * c.tok_bytes : 0);
     if (ok) t.valid |= 1 << x;
     const __amdgpu_buffer_rsrc_t rk = tile_rsrc(c.kplane + off, bytes);
     const __amdgpu_buffer_rsrc_t rv = tile_rsrc(c.vplane + off, bytes);
@@ -505,14 +510,24 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
       j_b = ok_b ? n / p.n_rep : 0;
       hq_b = h * p.n_rep + (ok_b ? n - j_b * p.n_rep : 0);
     };
-    // query operand loads through a descriptor over the sequence's query rows
-    auto load_q = [&](int bb, int64_t qoff_b, int j_b, int hq_b, bool live, u32x4 (&qo)[Tile::KS]) {
-      const char* qb = (const char*)((const T*)p.q + (int64_t)bb * p.q_sb + qoff_b * p.q_st);
+    // query operand loads through a descriptor over the sequence's query rows (none
+    // when !live, rows of lanes with !row_live read as zero). The descriptor is kept
+    // wave-uniform (base and size through readfirstlane, the rows masked after the
+    // load): a per-lane descriptor makes the compiler wrap every load in a waterfall
+    // loop, issued once per distinct descriptor.
+    auto load_q = [&](int bb, int64_t qoff_b, int j_b, int hq_b, bool live, bool row_live,
+                      u32x4 (&qo)[Tile::KS]) {
+      const uint64_t qa = (uint64_t)((const T*)p.q + (int64_t)bb * p.q_sb + qoff_b * p.q_st);
+      const char* qb = (const char*)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(qa >> 32)) << 32) |
+                                     (uint32_t)__builtin_amdgcn_readfirstlane((int)qa));
       const int qv = (int)(((int64_t)j_b * p.q_st + (int64_t)hq_b * p.q_sh) * (int64_t)sizeof(T)) + 16 * g;
-      const __amdgpu_buffer_rsrc_t rq = tile_rsrc(qb, live ? 0x7fffffff : 0);
+      const __amdgpu_buffer_rsrc_t rq = tile_rsrc(qb, __builtin_amdgcn_readfirstlane(live ? 0x7fffffff : 0));
+      const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int s2 = 0; s2 < Tile::KS; ++s2)
-        qo[s2] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, qv + 64 * s2, 0, 0));
+      for (int s2 = 0; s2 < Tile::KS; ++s2) {
+        const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, qv + 64 * s2, 0, 0));
+        qo[s2] = row_live ? v : zero;
+      }
     };
 
     int qlen, j, hq;
@@ -523,7 +538,7 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
     int kvt = seq_kvt(b);
     ScalarTableCtx tc = seq_ctx(b, kvt);
     u32x4 qop[Tile::KS], qn[Tile::KS];
-    load_q(b, qoff, j, hq, true, qop);
+    load_q(b, qoff, j, hq, true, true, qop);
     DecodeTile<T, D> ta, tb;
     int pha[2], phb[2], phn[2];
     fetch_phys(p, tc, pos - c, pha);
@@ -574,7 +589,7 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
         ph[0] = in_seg ? ph_in[0] : (look ? phn[0] : -1);
         ph[1] = in_seg ? ph_in[1] : (look ? phn[1] : -1);
         load_pair_scalar<T, D, AUX>(p, tg, in_seg ? pi_ + 1 : 0, ph, voff_k, voff_v, dst);
-        load_q(look ? nb : b, look ? qoff_n : qoff, look ? j_n : j, look ? hq_n : hq, look && ok_n, qn);
+        load_q(look ? nb : b, look ? qoff_n : qoff, look ? j_n : j, look ? hq_n : hq, look, ok_n, qn);
       };
 
       int pi = seg0;
