@@ -473,9 +473,11 @@ __global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
 //     end of the buffer: they return zeros without touching memory, and the loop
 //     needs no branch.
 //   - The loop is VALU-bound rather than MFMA- or memory-bound: per stage and wave
-//     (MT = NS = 4) 64 MFMAs against about 340 VALU instructions -- the nibble
+//     (MT = NS = 4) 64 MFMAs against about 300 VALU instructions -- the nibble
 //     unpack (8 per 32-bit word), the fold (2 FMAs per accumulator element) and the
-//     activation staging. With loads and stores taken out it still took 48 us of the
+//     activation staging (its row sums as v_dot2 against ones: 48 fewer per stage
+//     than converting and adding each value, 124.6 -> 118.5 us for the C5 layer at
+//     m = 64, no change at m = 256). With loads and stores taken out it still took 48 us of the
 //     4096 x 28672, m = 256 linear's 101 us; prefetching activations PF stages ahead
 //     as well changed nothing.
 //   - Per 32-key step the MFMA accumulates G = sum x (MAGIC + q) for every
@@ -587,6 +589,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int u = 0; u < MT; ++u)
       xr[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, x_off[u], so, 0));
   };
+  // the chunk's sum as four v_dot2 against a pair of ones (fp32 accumulation): a quarter
+  // of the instructions of converting and adding the eight values one by one
+  const uint32_t one2 = in_vgpr(E::kOnePair);
   auto stage_x = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < MT; ++u) {
@@ -594,7 +599,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const int r = q >> 4, c = q & 15;
       float sum = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sum += E::to_f32(xr[u][j] & 0xFFFFu) + E::to_f32(xr[u][j] >> 16);
+      for (int j = 0; j < 4; ++j) sum = dot2_acc<T>(xr[u][j], one2, sum);
       sum = row16_sum(sum);  // the 16 chunks of row r sit in one DPP row
       store16(&s_x[buf][r][8 * c], permute_x(xr[u]));
       // every lane of the row stores the same total: no branch, so the loop body stays
