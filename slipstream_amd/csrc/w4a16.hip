@@ -739,17 +739,19 @@ __global__ __launch_bounds__(LB) void w4a16_skinny_kernel(const W4Params p) {
   const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.sc, (uint32_t)((int64_t)p.n * p.groups * esize));
   const __amdgpu_buffer_rsrc_t rzp = buffer_rsrc(p.qz, (uint32_t)((int64_t)p.n * p.groups * 4));
   // ST fp32 scales, or ST 16-bit scales from the dword holding the first (ST / 2 + 1
-  // dwords cover them whether that one starts at a low or a high half)
-  uint32_t sdw[NS][ST + 1];
+  // dwords cover them whether that one starts at a low or a high half). The same NSD
+  // dwords are loaded for every scale dtype (the extra ones lie in the array or read as
+  // zero past it): a load under a dtype condition made the compiler wait for it before
+  // the stream's loads were issued, one memory round trip per call.
+  constexpr int NSD = ST >= 2 ? ST : 1;
+  uint32_t sdw[NS][NSD];
   int zv[NS][ST];
-  const int nsd = esize == 4 ? ST : ST / 2 + 1;
 #pragma unroll
   for (int ns = 0; ns < NS; ++ns) {
     const int gi = min(n0 + 16 * ns + ln, p.n - 1) * p.groups + k0 / 128;
 #pragma unroll
-    for (int d = 0; d <= ST; ++d)
-      sdw[ns][d] =
-          d < nsd ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsc, (gi * esize & ~3) + 4 * d, 0, 0) : 0u;
+    for (int d = 0; d < NSD; ++d)
+      sdw[ns][d] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rsc, (gi * esize & ~3) + 4 * d, 0, 0);
 #pragma unroll
     for (int i = 0; i < ST; ++i) zv[ns][i] = __builtin_amdgcn_raw_buffer_load_b32(rzp, (gi + i) * 4, 0, 0);
   }
