@@ -371,8 +371,11 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
   int* rec = p.ws_rec + (int64_t)blockIdx.x * 8;
 
   // ---- plan: total pairs, this range, and the sequence holding its first pair
-  int local = 0;
-  for (int b = tid; b < p.batch; b += blockDim.x) local += decode_pairs(p, b);
+  // pair count of this thread's first sequence, kept for the scan's first pass (one
+  // memory round trip less before the stream starts when the batch fits one pass)
+  const int v_first = tid < p.batch ? decode_pairs(p, tid) : 0;
+  int local = v_first;
+  for (int b = tid + blockDim.x; b < p.batch; b += blockDim.x) local += decode_pairs(p, b);
   // the plan's values are wave-uniform (block reductions); readfirstlane tells the
   // compiler so, which keeps the pair loop's scalars and buffer descriptors in SGPRs
   const int total = __builtin_amdgcn_readfirstlane(block_sum(local, s_red));
@@ -390,7 +393,7 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
   int run = 0;
   for (int base = 0; base < p.batch; base += blockDim.x) {
     const int b = base + tid;
-    const int v = b < p.batch ? decode_pairs(p, b) : 0;
+    const int v = base == 0 ? v_first : (b < p.batch ? decode_pairs(p, b) : 0);
     int tot;
     const int incl = block_incl_scan(v, s_red, tot);
     const int cb = run + incl - v;
