@@ -74,13 +74,20 @@ constexpr int kDecodeRows = 16;
 // Keys per decode iteration: two 16-token MFMA tiles.
 constexpr int kPairTokens = 32;
 
+// cu_seqlens and context_lens are read through the constant address space: where the
+// sequence index is wave-uniform that makes them scalar loads, whose waits (lgkmcnt)
+// leave the vector loads in flight alone -- a vector load of them inside the decode's
+// pipelined loop came with a wait for every K/V load in flight.
+typedef const __attribute__((address_space(4))) int32_t* ConstI32;
+
 __device__ __forceinline__ void seq_queries(const AttnParams& p, int b, int& qlen, int64_t& qoff) {
   if (p.chunk_tokens > 0) {
     qlen = p.q_period;
     qoff = (int64_t)b * p.q_period;
   } else if (p.cu) {
-    const int s = min(max(p.cu[b], 0), p.total_tokens);
-    const int e = min(max(p.cu[b + 1], s), p.total_tokens);
+    const ConstI32 cu = (ConstI32)p.cu;
+    const int s = min(max(cu[b], 0), p.total_tokens);
+    const int e = min(max(cu[b + 1], s), p.total_tokens);
     qlen = e - s;
     qoff = s;
   } else {
@@ -99,7 +106,7 @@ __device__ __forceinline__ int64_t lse_index(const AttnParams& p, int b, int64_t
 // KV length of sequence b (context_lens / seq_lens, negative counts as 0).
 __device__ __forceinline__ int kv_len(const AttnParams& p, int b) {
   if (p.chunk_tokens > 0) return min(p.chunk_tokens, p.prefix_tokens - b * p.chunk_tokens);
-  const int c = p.ctx_lens[b] - p.ctx_shift;
+  const int c = ((ConstI32)p.ctx_lens)[b] - p.ctx_shift;
   return c < 0 ? 0 : c;
 }
 
