@@ -582,26 +582,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int q = threadIdx.x + 256 * u;
     x_off[u] = (int)(((int64_t)min(q >> 4, rows - 1) * p.x_stride + 8 * (q & 15)) * (int64_t)sizeof(T));
   }
-  u32x4 xr[MT];
-  auto load_x = [&](int i) {
+  // two activation stages in registers: stage i + 2 is requested while stage i + 1 is
+  // still in flight, ahead of that stage's weight loads, so the wait for an activation
+  // stage (the vector-memory counter retires in order) never covers weights issued
+  // less than two stages earlier
+  u32x4 xr[2][MT];
+  auto load_x = [&](int i, u32x4 (&dst)[MT]) {
     const int so = i < i1 ? i * 128 * (int)sizeof(T) : kOutOfRange;
 #pragma unroll
     for (int u = 0; u < MT; ++u)
-      xr[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, x_off[u], so, 0));
+      dst[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, x_off[u], so, 0));
   };
   // the chunk's sum as four v_dot2 against a pair of ones (fp32 accumulation): a quarter
   // of the instructions of converting and adding the eight values one by one
   const uint32_t one2 = in_vgpr(E::kOnePair);
-  auto stage_x = [&](int buf) {
+  auto stage_x = [&](int buf, const u32x4 (&src)[MT]) {
 #pragma unroll
     for (int u = 0; u < MT; ++u) {
       const int q = threadIdx.x + 256 * u;
       const int r = q >> 4, c = q & 15;
       float sum = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sum = dot2_acc<T>(xr[u][j], one2, sum);
+      for (int j = 0; j < 4; ++j) sum = dot2_acc<T>(src[u][j], one2, sum);
       sum = row16_sum(sum);  // the 16 chunks of row r sit in one DPP row
-      store16(&s_x[buf][r][8 * c], permute_x(xr[u]));
+      store16(&s_x[buf][r][8 * c], permute_x(src[u]));
       // every lane of the row stores the same total: no branch, so the loop body stays
       // one block (a block boundary lets the compiler sink the folds to the loop end,
       // keeping every stage's partial sums live)
@@ -644,50 +648,83 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   };
 
+  // the first two activation stages, then the weight prologue: staging stage i0 waits
+  // for its own activations and the scale table, not for PF stages of weights
+  load_x(i0, xr[0]);
+  load_x(i0 + 1, xr[1]);
   u32x4 ring[PF][NS];
 #pragma unroll
   for (int u = 0; u < PF; ++u) load_w(i0 + u, ring[u]);
-  load_x(i0);
   table_store(threadIdx.x);
   for (int q0 = threadIdx.x + TB * 256; q0 < total; q0 += TB * 256) {  // large tables only
     table_load(q0);
     table_store(q0);
   }
-  stage_x(0);
+  stage_x(0, xr[0]);
   __syncthreads();  // the scale table and the first activation stage
   for (int i = i0; i < i1; i += PF) {
 #pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      const int buf = (i - i0 + u) & 1;
-      load_x(i + u + 1);
+    for (int u = 0; u < PF; ++u) {  // PF is even: stage i + u stages from xr[u & 1]
+      const int buf = u & 1;
+      load_x(i + u + 2, xr[u & 1]);
       __builtin_amdgcn_sched_barrier(0);
       compute(i + u, buf, ring[u]);
       __builtin_amdgcn_sched_barrier(0);
       load_w(i + u + PF, ring[u]);
       __builtin_amdgcn_sched_barrier(0);
-      stage_x(buf ^ 1);
+      stage_x(buf ^ 1, xr[(u + 1) & 1]);
       __syncthreads();
     }
   }
 
+  // Results through LDS -- the activation stages' bytes, free after the loop's last
+  // barrier -- so that each thread writes 16 contiguous bytes of a row (4-byte stores
+  // spread over four rows per instruction took ~1.8 us to issue at m = 64), in passes
+  // of MTP activation tiles where the whole tile does not fit.
   // lane holds C[m0 + mt*16 + 4kg + e][n0 + ns*16 + ln]
+  constexpr int TW = 64 * NS;                                    // the workgroup's columns
+  constexpr int TROW = TW + 4;                                   // LDS row, floats (skewed)
+  constexpr int PR = (int)(sizeof(s_x) / (TROW * sizeof(float))) / 16 * 16;
+  constexpr int MTP = PR / 16 < MT ? PR / 16 : MT;               // activation tiles per pass
+  static_assert(MTP >= 1, "a 16-row tile of results fits the activation stages");
+  float* const s_t = reinterpret_cast<float*>(&s_x[0][0][0]);
   const bool split = ks > 1;
+  const bool vec_n = p.n % 4 == 0;
+  const bool vec_out = vec_n && p.o_stride % 4 == 0 && ((uintptr_t)p.out & 7) == 0;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int mt0 = 0; mt0 < MT; mt0 += MTP) {
+    if (mt0 > 0) __syncthreads();  // the previous pass has been read
 #pragma unroll
-    for (int ns = 0; ns < NS; ++ns) {
-      const int n = n0 + ns * 16 + ln;
+    for (int mt = mt0; mt < mt0 + MTP && mt < MT; ++mt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = m0 + mt * 16 + 4 * kg + e;
-        if (m < p.m && n < p.n) {
+      for (int ns = 0; ns < NS; ++ns)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          s_t[(16 * (mt - mt0) + 4 * kg + e) * TROW + wave * 16 * NS + 16 * ns + ln] = acc[mt][ns][e];
+    __syncthreads();
+    for (int q = threadIdx.x; q < MTP * 16 * (TW / 4); q += 256) {
+      const int rl = q / (TW / 4), c4 = q - rl * (TW / 4);
+      const int m = m0 + 16 * mt0 + rl, n = nb + 4 * c4;
+      if (m >= p.m || n >= p.n) continue;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&s_t[rl * TROW + 4 * c4]);
+      if (split && vec_n) {
+        *reinterpret_cast<f32x4*>(part + ((int64_t)zr * p.m + m) * p.n + n) = v;
+      } else if (!split && vec_out) {
+        T* const o = (T*)p.out + (int64_t)m * p.o_stride + n;
+        const T h[4] = {(T)v[0], (T)v[1], (T)v[2], (T)v[3]};
+        *reinterpret_cast<u32x2*>(o) = __builtin_bit_cast(u32x2, h);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (n + e >= p.n) break;
           if (split)
-            part[((int64_t)zr * p.m + m) * p.n + n] = acc[mt][ns][e];
+            part[((int64_t)zr * p.m + m) * p.n + n + e] = v[e];
           else
-            ((T*)p.out)[(int64_t)m * p.o_stride + n] = (T)acc[mt][ns][e];
+            ((T*)p.out)[(int64_t)m * p.o_stride + n + e] = (T)v[e];
         }
       }
     }
+  }
 }
 
 // Skinny kernel (2 <= m <= 16, g == 128): bandwidth-bound shapes without a K split
