@@ -311,8 +311,9 @@ int ss_build_step_metadata(const int32_t* block_tables, int64_t bt_stride, int m
  * (rmsnorm.py:30-33, fused_rmsnorm.py:73-82): s = x + residual in dtype,
  * out = weight * dtype(s * rsqrt(mean(s^2) + eps)) with the variance in fp32.
  * x, residual (or NULL), out: [rows, cols] with row strides in elements; weight
- * [cols]. 16-byte aligned rows, cols a multiple of 8 (16-bit) or 4 (fp32), at
- * most 16384 (16-bit) columns; otherwise SS_ERR_UNSUPPORTED.
+ * [cols]. 16-byte aligned rows, cols a multiple of 8 (16-bit) or 4 (fp32);
+ * otherwise SS_ERR_UNSUPPORTED. Rows of up to 2048 16-byte pieces are held in
+ * registers; longer ones are read twice.
  */
 int ss_rmsnorm(const void* x, const void* residual, const void* weight, void* out, int64_t rows, int cols,
                int64_t x_stride, int64_t r_stride, int64_t o_stride, float eps, int dtype, void* stream);

@@ -128,6 +128,50 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const NormArgs a) {
   }
 }
 
+// Rows longer than the register-resident variants hold (more than 256 * 8 pieces):
+// two passes over the row in memory -- the sum of squares, then the normalised
+// output -- reading x (and the residual) twice. Each thread adds its pieces in the
+// same order as rmsnorm_kernel (pc = tid, tid + 256, ...), then the same reduction.
+template <typename T>
+__global__ __launch_bounds__(256) void rmsnorm_long_kernel(const NormArgs a) {
+  constexpr int EPP = 16 / sizeof(T);
+  __shared__ float s_part[4];
+  const int64_t row = blockIdx.x;
+  const char* xr = a.x + row * a.x_stride;
+  const char* rr = a.res ? a.res + row * a.r_stride : nullptr;
+  const int pieces = a.cols / EPP;
+  auto load_row = [&](int pc, float (&v)[EPP]) {
+    unpack<T>(*reinterpret_cast<const ss::u32x4*>(xr + (int64_t)pc * 16), v);
+    if (rr) {
+      float rv[EPP];
+      unpack<T>(*reinterpret_cast<const ss::u32x4*>(rr + (int64_t)pc * 16), rv);
+#pragma unroll
+      for (int e = 0; e < EPP; ++e) v[e] = Rnd<T>::r(pin(v[e] + rv[e]));
+    }
+  };
+  float ss = 0.f;
+  for (int pc = threadIdx.x; pc < pieces; pc += 256) {
+    float v[EPP];
+    load_row(pc, v);
+#pragma unroll
+    for (int e = 0; e < EPP; ++e) ss += pin(v[e] * v[e]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float mean = (s_part[0] + s_part[1] + s_part[2] + s_part[3]) / (float)a.cols;
+  const float rstd = 1.0f / __builtin_sqrtf(mean + a.eps);
+  for (int pc = threadIdx.x; pc < pieces; pc += 256) {
+    float v[EPP], wv[EPP], o[EPP];
+    load_row(pc, v);
+    unpack<T>(*reinterpret_cast<const ss::u32x4*>(a.w + (int64_t)pc * 16), wv);
+#pragma unroll
+    for (int e = 0; e < EPP; ++e) o[e] = Rnd<T>::r(pin(wv[e] * Rnd<T>::r(pin(v[e] * rstd))));
+    *reinterpret_cast<ss::u32x4*>(a.y + row * a.y_stride + (int64_t)pc * 16) = pack<T>(o);
+  }
+}
+
 struct SwigluArgs {
   const char* g;
   const char* u;
@@ -168,8 +212,10 @@ int launch_rmsnorm(const NormArgs& a, int64_t rows, hipStream_t s) {
     hipLaunchKernelGGL((rmsnorm_kernel<T, 2>), dim3((unsigned)rows), dim3(256), 0, s, a);
   else if (pieces <= 1024)
     hipLaunchKernelGGL((rmsnorm_kernel<T, 4>), dim3((unsigned)rows), dim3(256), 0, s, a);
-  else
+  else if (pieces <= 2048)
     hipLaunchKernelGGL((rmsnorm_kernel<T, 8>), dim3((unsigned)rows), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((rmsnorm_long_kernel<T>), dim3((unsigned)rows), dim3(256), 0, s, a);
   return ss_host::launch_status("rmsnorm");
 }
 
@@ -194,11 +240,9 @@ extern "C" int ss_rmsnorm(const void* x, const void* residual, const void* weigh
   }
   const int es = dtype == SS_DTYPE_F32 ? 4 : 2;
   const int epp = 16 / es;
-  if (cols % epp != 0 || cols / epp > 256 * 8 || !al16(x) || !al16(weight) || !al16(out) ||
-      (residual && !al16(residual)) || (x_stride * es) % 16 || (o_stride * es) % 16 ||
-      (residual && (r_stride * es) % 16) || rows > 0x7fffffff) {
-    ss_host::set_error("%s: rows must be 16-byte aligned with %d-element multiples, at most %d columns", who, epp,
-                       256 * 8 * epp);
+  if (cols % epp != 0 || !al16(x) || !al16(weight) || !al16(out) || (residual && !al16(residual)) ||
+      (x_stride * es) % 16 || (o_stride * es) % 16 || (residual && (r_stride * es) % 16) || rows > 0x7fffffff) {
+    ss_host::set_error("%s: rows must be 16-byte aligned with %d-element multiples", who, epp);
     return SS_ERR_UNSUPPORTED;
   }
   NormArgs a;
