@@ -486,16 +486,20 @@ __global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
 // Every range is a whole number of PF stages (host-checked).
 constexpr int kOutOfRange = 0x40000000;  // buffer offset past any operand (< 2^31 bytes)
 
-template <typename T, int MT, int NS, int PF>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void w4a16_tile_kernel(
+template <typename T, int MT, int NS, int PF, int WV>
+__global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2))) void w4a16_tile_kernel(
     const W4Params p, float* __restrict__ part, int kchunk, int ks, int n_tiles, int m_blocks) {
   typedef W4Elem<T> E;
+  constexpr int NTHR = 64 * WV;       // threads
+  constexpr int TR = 16 * NS * WV;    // weight rows of the workgroup
+  constexpr int XC = 256 * MT / NTHR; // activation-stage chunks per thread
+  static_assert(XC >= 1 && 256 * MT % NTHR == 0, "every thread stages whole chunks");
   constexpr int BM = 16 * MT;
   constexpr int LROW = 128 + 8;  // LDS row of an activation stage, elements (16-byte skew)
   __shared__ __attribute__((aligned(16))) T s_x[2][BM][LROW];
   __shared__ __attribute__((aligned(16))) float s_sum[2][BM];
   extern __shared__ __attribute__((aligned(16))) char s_dyn[];
-  float2* const s_sz = (float2*)s_dyn;  // [64*NS rows][gr + 1] (s, s*(MAGIC+z))
+  float2* const s_sz = (float2*)s_dyn;  // [TR rows][gr + 1] (s, s*(MAGIC+z))
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -512,7 +516,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int pair = blk * 8 + (within & 7);
   if (pair >= ks * n_tiles) return;
   const int zr = pair % ks;
-  const int nb = (pair / ks) * 64 * NS;  // the workgroup's first weight row
+  const int nb = (pair / ks) * TR;       // the workgroup's first weight row
   const int n0 = nb + wave * 16 * NS;   // this wave's
   const int m0 = (within >> 3) * BM;
   const int rows = min(BM, p.m - m0);
@@ -531,13 +535,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const uint32_t f16_mask = p.sdt == SS_DTYPE_F16 ? ~0u : 0u, bf16_mask = p.sdt == SS_DTYPE_BF16 ? ~0u : 0u;
   const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.sc, (uint32_t)((int64_t)p.n * p.groups * esize));
   const __amdgpu_buffer_rsrc_t rzp = buffer_rsrc(p.qz, (uint32_t)((int64_t)p.n * p.groups * 4));
-  const int total = 64 * NS * gr;
+  const int total = TR * gr;
   uint32_t sbits[TB];
   int zv[TB];
   auto table_load = [&](int q0) {
 #pragma unroll
     for (int u = 0; u < TB; ++u) {
-      const int q = min(q0 + 256 * u, total - 1);
+      const int q = min(q0 + NTHR * u, total - 1);
       const int r = q / gr, gl = q - r * gr;
       const int si = min(nb + r, p.n - 1) * p.groups + g0 + gl;
       sbits[u] = scale_bits(rsc, si, esize);
@@ -547,7 +551,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   auto table_store = [&](int q0) {
 #pragma unroll
     for (int u = 0; u < TB; ++u) {
-      const int q = q0 + 256 * u;
+      const int q = q0 + NTHR * u;
       if (q < total) {
         const int r = q / gr, gl = q - r * gr;
         const float sc = decode_scale_masked(sbits[u], f16_mask, bf16_mask);
@@ -572,34 +576,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       w[ns] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, w_off[ns], so, kNonTemporal));
   };
 
-  // activation staging: chunk q = threadIdx.x + 256 u is row q / 16, keys 8 (q % 16)..+7
+  // activation staging: chunk q = threadIdx.x + NTHR u is row q / 16, keys 8 (q % 16)..+7
   // of the stage; rows past M read row M-1 (their outputs are never stored)
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(
       (const T*)p.x + (int64_t)m0 * p.x_stride, (uint32_t)(((int64_t)(rows - 1) * p.x_stride + p.k) * sizeof(T)));
-  int x_off[MT];
+  int x_off[XC];
 #pragma unroll
-  for (int u = 0; u < MT; ++u) {
-    const int q = threadIdx.x + 256 * u;
+  for (int u = 0; u < XC; ++u) {
+    const int q = threadIdx.x + NTHR * u;
     x_off[u] = (int)(((int64_t)min(q >> 4, rows - 1) * p.x_stride + 8 * (q & 15)) * (int64_t)sizeof(T));
   }
   // two activation stages in registers: stage i + 2 is requested while stage i + 1 is
   // still in flight, ahead of that stage's weight loads, so the wait for an activation
   // stage (the vector-memory counter retires in order) never covers weights issued
   // less than two stages earlier
-  u32x4 xr[2][MT];
-  auto load_x = [&](int i, u32x4 (&dst)[MT]) {
+  u32x4 xr[2][XC];
+  auto load_x = [&](int i, u32x4 (&dst)[XC]) {
     const int so = i < i1 ? i * 128 * (int)sizeof(T) : kOutOfRange;
 #pragma unroll
-    for (int u = 0; u < MT; ++u)
+    for (int u = 0; u < XC; ++u)
       dst[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, x_off[u], so, 0));
   };
   // the chunk's sum as four v_dot2 against a pair of ones (fp32 accumulation): a quarter
   // of the instructions of converting and adding the eight values one by one
   const uint32_t one2 = in_vgpr(E::kOnePair);
-  auto stage_x = [&](int buf, const u32x4 (&src)[MT]) {
+  auto stage_x = [&](int buf, const u32x4 (&src)[XC]) {
 #pragma unroll
-    for (int u = 0; u < MT; ++u) {
-      const int q = threadIdx.x + 256 * u;
+    for (int u = 0; u < XC; ++u) {
+      const int q = threadIdx.x + NTHR * u;
       const int r = q >> 4, c = q & 15;
       float sum = 0.f;
 #pragma unroll
@@ -656,7 +660,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
   for (int u = 0; u < PF; ++u) load_w(i0 + u, ring[u]);
   table_store(threadIdx.x);
-  for (int q0 = threadIdx.x + TB * 256; q0 < total; q0 += TB * 256) {  // large tables only
+  for (int q0 = threadIdx.x + TB * NTHR; q0 < total; q0 += TB * NTHR) {  // large tables only
     table_load(q0);
     table_store(q0);
   }
@@ -682,7 +686,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // spread over four rows per instruction took ~1.8 us to issue at m = 64), in passes
   // of MTP activation tiles where the whole tile does not fit.
   // lane holds C[m0 + mt*16 + 4kg + e][n0 + ns*16 + ln]
-  constexpr int TW = 64 * NS;                                    // the workgroup's columns
+  constexpr int TW = TR;                                         // the workgroup's columns
   constexpr int TROW = TW + 4;                                   // LDS row, floats (skewed)
   constexpr int PR = (int)(sizeof(s_x) / (TROW * sizeof(float))) / 16 * 16;
   constexpr int MTP = PR / 16 < MT ? PR / 16 : MT;               // activation tiles per pass
@@ -702,7 +706,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int e = 0; e < 4; ++e)
           s_t[(16 * (mt - mt0) + 4 * kg + e) * TROW + wave * 16 * NS + 16 * ns + ln] = acc[mt][ns][e];
     __syncthreads();
-    for (int q = threadIdx.x; q < MTP * 16 * (TW / 4); q += 256) {
+    for (int q = threadIdx.x; q < MTP * 16 * (TW / 4); q += NTHR) {
       const int rl = q / (TW / 4), c4 = q - rl * (TW / 4);
       const int m = m0 + 16 * mt0 + rl, n = nb + 4 * c4;
       if (m >= p.m || n >= p.n) continue;
@@ -1502,12 +1506,18 @@ int launch_w4a16_x(const W4Params& p, const W4Plan& pl, hipStream_t stream) {
   return ss_host::launch_status("w4a16 gemm");
 }
 
-template <typename T, int MT, int NS, int PF>
+// NS weight tiles per wave, WV waves: the plan's 64 * pl.ns rows per workgroup are
+// 16 * NS * WV
+template <typename T, int MT, int NS, int PF, int WV>
 int launch_w4a16_tile(const W4Params& p, const W4Plan& pl, float* part, hipStream_t stream) {
+  if (16 * NS * WV != 64 * pl.ns) {
+    ss_host::set_error("w4a16 gemm: tiled plan of %d rows per workgroup, kernel of %d", 64 * pl.ns, 16 * NS * WV);
+    return SS_ERR_UNSUPPORTED;
+  }
   static bool attr_set = false;  // per instantiation; the attribute is process-wide
   if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)w4a16_tile_kernel<T, MT, NS, PF>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            kTileTableMax) != hipSuccess) {
+    if (hipFuncSetAttribute((const void*)w4a16_tile_kernel<T, MT, NS, PF, WV>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kTileTableMax) != hipSuccess) {
       ss_host::set_error("w4a16 gemm: cannot reserve %d bytes of LDS", kTileTableMax);
       return SS_ERR_UNSUPPORTED;
     }
@@ -1519,8 +1529,8 @@ int launch_w4a16_tile(const W4Params& p, const W4Plan& pl, float* part, hipStrea
     ss_host::set_error("w4a16 gemm: %lld tiled workgroups", (long long)grid);
     return SS_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((w4a16_tile_kernel<T, MT, NS, PF>), dim3((unsigned)grid), dim3(256), pl.lds, stream, p, part,
-                     pl.kchunk, pl.ks, pl.n_tiles, pl.m_blocks);
+  hipLaunchKernelGGL((w4a16_tile_kernel<T, MT, NS, PF, WV>), dim3((unsigned)grid), dim3(64 * WV), pl.lds, stream, p,
+                     part, pl.kchunk, pl.ks, pl.n_tiles, pl.m_blocks);
   int st = ss_host::launch_status("w4a16 gemm (tiled)");
   if (st != SS_OK || pl.ks == 1) return st;
   const bool vec = p.n % 4 == 0;
@@ -1630,10 +1640,21 @@ int launch_w4a16_typed(const W4Params& p, const W4Plan& pl, float* part, hipStre
   if (pl.narrow == 4) return launch_w4a16_narrow_mr<T, 4>(p, pl, stream);
   if (pl.skinny) return launch_w4a16_skinny_mt<T, 1>(p, pl, stream);
   if (pl.tile) {
-    if (pl.mt == 1) return launch_w4a16_tile<T, 1, 2, 8>(p, pl, part, stream);
-    if (pl.mt == 2) return launch_w4a16_tile<T, 2, 2, 8>(p, pl, part, stream);
-    if (pl.ns == 2) return launch_w4a16_tile<T, 4, 2, 4>(p, pl, part, stream);
-    return launch_w4a16_tile<T, 4, 4, 2>(p, pl, part, stream);
+    // A grid of one workgroup per CU at most (m <= 64 but the widest linears) takes eight
+    // waves of half the rows each: two waves per SIMD instead of one, so one wave's MFMAs
+    // overlap the other's unpack, fold and staging (C5 at m = 32: 5-6 % faster, m = 64:
+    // 1-3 %). Larger grids keep four waves: two of their workgroups share a CU (gate_up at
+    // m = 32 and 64 took 11-17 % longer with eight, m = 256 3-10 %).
+    const int64_t grid = ((int64_t)pl.ks * pl.n_tiles + 7) / 8 * 8 * pl.m_blocks;
+    const bool eight = grid <= ss_host::device_cu_count();
+    if (pl.mt == 1) return launch_w4a16_tile<T, 1, 2, 8, 4>(p, pl, part, stream);
+    if (pl.mt == 2)
+      return eight ? launch_w4a16_tile<T, 2, 1, 8, 8>(p, pl, part, stream)
+                   : launch_w4a16_tile<T, 2, 2, 8, 4>(p, pl, part, stream);
+    if (pl.ns == 2)
+      return eight ? launch_w4a16_tile<T, 4, 1, 4, 8>(p, pl, part, stream)
+                   : launch_w4a16_tile<T, 4, 2, 4, 4>(p, pl, part, stream);
+    return launch_w4a16_tile<T, 4, 4, 2, 4>(p, pl, part, stream);
   }
   if (pl.gemv) {
     if (p.k <= 8192)
