@@ -217,13 +217,17 @@ int ss_paged_attention_shared_prefix(const void* q, void* out, const void* k_cac
  * of LDS: k/group_size <= 480 for m <= 16) take the MFMA kernels (m = 1: a
  * bandwidth GEMV; m >= 2 with group_size % 128 == 0: a tiled kernel that may
  * split K over workgroups); everything else a scalar fp32 kernel. The result
- * does not depend on timing: split-K partials are added in a fixed order by a
- * second kernel, never by atomics.
+ * does not depend on timing: split-K partials are added in range order, by a
+ * second kernel or (two ranges, m <= 64) by the last range of each output tile
+ * to finish, which a device-scope compare-and-swap on a tagged arrival word in
+ * the workspace identifies; never by atomic adds.
  * workspace: ss_w4a16_workspace_size() reports the bytes of the split-K
- * partials (ranges * m * n floats; 0 when the plan does not split). Pass at
- * least that many bytes, 16-byte aligned; with less (or NULL, 0) the call still
- * succeeds on the untiled MFMA kernel, which needs no scratch. Calls that share
- * one workspace must be ordered on one stream.
+ * partials (ranges * m * n floats) and the arrival words after them (8 bytes
+ * per output tile); 0 when the plan does not split. Pass at least that many
+ * bytes, 16-byte aligned, with any contents (each call tags its words, and the
+ * last range leaves them zero); with less (or NULL, 0) the call still succeeds
+ * on the untiled MFMA kernel, which needs no scratch. Calls that share one
+ * workspace must be ordered on one stream.
  */
 int ss_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int group_size, int act_dtype,
                             int64_t* bytes);

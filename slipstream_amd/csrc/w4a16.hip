@@ -32,6 +32,8 @@
 //
 // Generic path (any other shape, fp32 activations): one thread per output,
 // fp32 dequant and dot product.
+#include <atomic>
+
 #include "ss_common.h"
 
 namespace ss {
@@ -52,6 +54,35 @@ constexpr int kMaxKW = 8;
 // Cache policy of the weight loads: non-temporal (every weight is read once per call;
 // streaming without cache allocation measured ~14 % more bandwidth on gfx950).
 constexpr int kNonTemporal = 2;
+// Cache policy sc1 (device scope): a store written through this XCD's L2 to the point of
+// device coherence, a load not served by possibly stale lines of this CU's or XCD's caches.
+constexpr int kDeviceScope = 16;
+
+// s_waitcnt vmcnt(0) with the other counters left alone (gfx9 encoding): every vector
+// memory operation of this wave, stores included, has completed
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8)); }
+
+// Arrival count of one output tile's K ranges in a 64-bit word: bits 8.. hold the call's
+// tag, bits 0..7 the ranges arrived. A word with another tag (an earlier call, or memory
+// never written) counts as zero arrivals, so the workspace needs no initialisation; the
+// last range resets the word to zero, which the first compare-and-swap of the next call
+// (or of a replayed launch: a captured graph passes the same tag again) expects.
+// No cache maintenance: the partials are device-scope stores the caller has waited for
+// (vmcnt 0) before it arrives, the count is a device-scope atomic, and the last range
+// reads the partials with device-scope loads. (Release/acquire fences at device scope
+// write back or invalidate a whole L2 per wave, several times slower.)
+__device__ __forceinline__ bool arrive_last(unsigned long long* word, unsigned long long tag, int ranges) {
+  unsigned long long old = 0ull;
+  unsigned long long now;
+  do {
+    const unsigned long long have = (old & ~0xFFull) == tag ? (old & 0xFFull) : 0ull;
+    now = tag | (have + 1);
+  } while (!__hip_atomic_compare_exchange_weak(word, &old, now, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT));
+  if ((int)(now & 0xFFull) != ranges) return false;
+  __hip_atomic_store(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
 
 template <typename T>
 struct W4Elem;
@@ -455,11 +486,12 @@ __global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
 // 64*NS weight rows (the kernel above reads it once per 16*NS rows, which made
 // activation traffic several times the weight traffic for m >= 16).
 //
-// A workgroup owns 16*MT activation rows and 64*NS weight rows (four waves of
-// 16*NS rows each, every wave against all 16*MT activation rows) over one range of
-// `kchunk` 128-key stages (blockIdx.z). With several ranges (split K) each writes
-// fp32 partials part[z][m][n] and w4a16_splitk_reduce_kernel adds them in range
-// order, so the result does not depend on timing.
+// A workgroup owns 16*MT activation rows and 16*NS*WV weight rows (WV waves of 16*NS
+// rows each, every wave against all 16*MT activation rows) over one range of `kchunk`
+// 128-key stages. With several ranges (split K) each writes fp32 partials
+// part[z][m][n]; w4a16_splitk_reduce_kernel adds them in range order, or, with arrival
+// words (two ranges at m <= 64), the last range of each output tile to finish adds them
+// itself in the same order, so the result does not depend on timing.
 //   - Once per workgroup: the scale table of its rows and range, as pairs
 //     (s, s * (MAGIC + z)) in LDS (dynamic shared memory). Per-stage scale loads
 //     from memory, 16 scattered words per instruction, took the memory pipeline
@@ -488,7 +520,8 @@ constexpr int kOutOfRange = 0x40000000;  // buffer offset past any operand (< 2^
 
 template <typename T, int MT, int NS, int PF, int WV>
 __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2))) void w4a16_tile_kernel(
-    const W4Params p, float* __restrict__ part, int kchunk, int ks, int n_tiles, int m_blocks) {
+    const W4Params p, float* __restrict__ part, unsigned long long* __restrict__ arrivals, unsigned long long tag,
+    int kchunk, int ks, int n_tiles, int m_blocks) {
   typedef W4Elem<T> E;
   constexpr int NTHR = 64 * WV;       // threads
   constexpr int TR = 16 * NS * WV;    // weight rows of the workgroup
@@ -693,8 +726,16 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
   static_assert(MTP >= 1, "a 16-row tile of results fits the activation stages");
   float* const s_t = reinterpret_cast<float*>(&s_x[0][0][0]);
   const bool split = ks > 1;
+  // with arrival words the last range finishes the tile (below); without, a second
+  // kernel adds the partials after this one
+  const bool fused = split && arrivals != nullptr;
   const bool vec_n = p.n % 4 == 0;
   const bool vec_out = vec_n && p.o_stride % 4 == 0 && ((uintptr_t)p.out & 7) == 0;
+  // this range's partials: rows [m0, m0 + BM) of range zr, through a descriptor over
+  // them (rows past M are never written); device-scope stores when this kernel finishes
+  // the tile
+  float* const pbase = part + ((int64_t)zr * p.m + m0) * p.n;
+  const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(pbase, (uint32_t)((int64_t)rows * p.n * 4));
 #pragma unroll
   for (int mt0 = 0; mt0 < MT; mt0 += MTP) {
     if (mt0 > 0) __syncthreads();  // the previous pass has been read
@@ -712,7 +753,11 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
       if (m >= p.m || n >= p.n) continue;
       const f32x4 v = *reinterpret_cast<const f32x4*>(&s_t[rl * TROW + 4 * c4]);
       if (split && vec_n) {
-        *reinterpret_cast<f32x4*>(part + ((int64_t)zr * p.m + m) * p.n + n) = v;
+        const int off = (int)(((int64_t)(m - m0) * p.n + n) * 4);
+        if (fused)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp, off, 0, kDeviceScope);
+        else
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp, off, 0, 0);
       } else if (!split && vec_out) {
         T* const o = (T*)p.out + (int64_t)m * p.o_stride + n;
         const T h[4] = {(T)v[0], (T)v[1], (T)v[2], (T)v[3]};
@@ -722,11 +767,74 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
         for (int e = 0; e < 4; ++e) {
           if (n + e >= p.n) break;
           if (split)
-            part[((int64_t)zr * p.m + m) * p.n + n + e] = v[e];
+            __hip_atomic_store(part + ((int64_t)zr * p.m + m) * p.n + n + e, v[e], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
           else
             ((T*)p.out)[(int64_t)m * p.o_stride + n + e] = (T)v[e];
         }
       }
+    }
+  }
+  if (!fused) return;
+
+  // K split: the last of the tile's ranges to arrive adds every range's partials in
+  // range order ((0 + p0) + p1 + ...: the same sums in the same order whichever range
+  // arrives last) and writes the output, so no second launch is needed
+  __shared__ int s_last;
+  wait_vm0();        // this thread's partials have reached the point of device coherence
+  __syncthreads();   // every thread's, before the count moves
+  if (threadIdx.x == 0) s_last = arrive_last(arrivals + (pair / ks) * m_blocks + (within >> 3), tag, ks) ? 1 : 0;
+  __syncthreads();
+  if (!s_last) return;
+  // each thread owns CPT 16-byte chunks (four columns of a row) of the BM x TW tile; the
+  // loads of range z + 1 are requested before range z is added (one memory round trip
+  // for the whole gather, not one per range)
+  constexpr int CPT = BM * TW / 4 / NTHR;
+  static_assert(CPT * NTHR * 4 == BM * TW, "the tile splits into whole chunks per thread");
+  const __amdgpu_buffer_rsrc_t rall = buffer_rsrc(part, (uint32_t)((int64_t)ks * p.m * p.n * 4));
+  int coff[CPT];  // byte offset of the chunk in range 0, or past every range (zeros)
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int q = threadIdx.x + NTHR * i;
+    const int rl = q / (TW / 4), c4 = q - rl * (TW / 4);
+    const int m = m0 + rl, n = nb + 4 * c4;
+    coff[i] = (m < p.m && n < p.n) ? (int)(((int64_t)m * p.n + n) * 4) : kOutOfRange;
+  }
+  const int zstride = (int)((int64_t)p.m * p.n * 4);
+  auto gather = [&](int z, u32x4 (&v)[CPT]) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i)
+      v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rall, coff[i], z < ks ? z * zstride : kOutOfRange, kDeviceScope));
+  };
+  f32x4 y[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) y[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 vcur[CPT], vnext[CPT];
+  gather(0, vcur);
+  for (int z = 0; z < ks; ++z) {
+    gather(z + 1, vnext);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const f32x4 v = __builtin_bit_cast(f32x4, vcur[i]);
+      y[i][0] += v[0], y[i][1] += v[1], y[i][2] += v[2], y[i][3] += v[3];
+      vcur[i] = vnext[i];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int q = threadIdx.x + NTHR * i;
+    const int rl = q / (TW / 4), c4 = q - rl * (TW / 4);
+    const int m = m0 + rl, n = nb + 4 * c4;
+    if (m >= p.m || n >= p.n) continue;
+    T* const o = (T*)p.out + (int64_t)m * p.o_stride + n;
+    if (vec_out) {
+      const T h[4] = {(T)y[i][0], (T)y[i][1], (T)y[i][2], (T)y[i][3]};
+      *reinterpret_cast<u32x2*>(o) = __builtin_bit_cast(u32x2, h);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < p.n) o[e] = (T)y[i][e];
     }
   }
 }
@@ -1369,6 +1477,8 @@ bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
   pl.ks = (int)((rounds + per - 1) / per);
   if (pl.ks > 65535) return false;
   pl.lds = tile_table_bytes(ns, pl.kchunk, g);
+  // the partials are addressed by 32-bit offsets, with kOutOfRange past all of them
+  if (pl.ks > 1 && (int64_t)pl.ks * m * n * 4 >= (int64_t)kOutOfRange) return false;
   return true;
 }
 
@@ -1419,8 +1529,11 @@ bool plan_skinny(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
   return true;
 }
 
+// Split-K workspace of the tiled kernel: the fp32 partials [ranges][m][n], then (256-byte
+// aligned) one 64-bit arrival word per output tile (weight tile x activation block).
+int64_t tile_part_bytes(const W4Plan& pl, int64_t m, int64_t n) { return ((int64_t)pl.ks * m * n * 4 + 255) / 256 * 256; }
 int64_t tile_workspace_bytes(const W4Plan& pl, int64_t m, int64_t n) {
-  return pl.tile && pl.ks > 1 ? (int64_t)pl.ks * m * n * 4 : 0;
+  return pl.tile && pl.ks > 1 ? tile_part_bytes(pl, m, n) + (int64_t)pl.n_tiles * pl.m_blocks * 8 : 0;
 }
 
 constexpr size_t kLdsBudget = 64 * 1024;  // LDS bytes per workgroup
@@ -1506,6 +1619,15 @@ int launch_w4a16_x(const W4Params& p, const W4Plan& pl, hipStream_t stream) {
   return ss_host::launch_status("w4a16 gemm");
 }
 
+// Tag of a split call's arrival words: a process-wide count, so that words left by earlier
+// calls (or never written) do not match.
+unsigned long long next_arrival_tag() {
+  static std::atomic<unsigned long long> count{0};
+  unsigned long long t = 0;
+  while (t == 0) t = (++count & ((1ull << 56) - 1)) << 8;
+  return t;
+}
+
 // NS weight tiles per wave, WV waves: the plan's 64 * pl.ns rows per workgroup are
 // 16 * NS * WV
 template <typename T, int MT, int NS, int PF, int WV>
@@ -1529,10 +1651,17 @@ int launch_w4a16_tile(const W4Params& p, const W4Plan& pl, float* part, hipStrea
     ss_host::set_error("w4a16 gemm: %lld tiled workgroups", (long long)grid);
     return SS_ERR_UNSUPPORTED;
   }
+  // Two ranges at m <= 64: the last range of each tile adds the two partials itself (C5
+  // gate and gate_up at m = 32 and 64: 7-9 % faster than a second kernel). With more
+  // ranges, or 64-row blocks of m = 256, that last workgroup's gather outlasts a reduce
+  // kernel spread over the whole GPU (o at m = 64, 8 ranges: 21.4 against 16.4 us).
+  const bool fused = pl.ks == 2 && p.m <= 64;
+  unsigned long long* const arrivals = fused ? (unsigned long long*)((char*)part + tile_part_bytes(pl, p.m, p.n)) : nullptr;
+  const unsigned long long tag = fused ? next_arrival_tag() : 0ull;
   hipLaunchKernelGGL((w4a16_tile_kernel<T, MT, NS, PF, WV>), dim3((unsigned)grid), dim3(64 * WV), pl.lds, stream, p,
-                     part, pl.kchunk, pl.ks, pl.n_tiles, pl.m_blocks);
+                     part, arrivals, tag, pl.kchunk, pl.ks, pl.n_tiles, pl.m_blocks);
   int st = ss_host::launch_status("w4a16 gemm (tiled)");
-  if (st != SS_OK || pl.ks == 1) return st;
+  if (st != SS_OK || pl.ks == 1 || fused) return st;
   const bool vec = p.n % 4 == 0;
   const int64_t threads = (int64_t)p.m * (vec ? p.n / 4 : p.n);
   const unsigned blocks = (unsigned)((threads + 255) / 256);

@@ -82,7 +82,9 @@ def test_w4a16_argument_errors_need_no_device():
     assert out.value == 0  # batch 1: the GEMV, no scratch
     # the tiled kernel splits K over workgroups: fp32 partials [ranges][m][n]
     assert lib.ss_w4a16_workspace_size(64, 4096, 14336, 128, _ffi.SS_DTYPE_BF16, ctypes.byref(out)) == _ffi.SS_OK
-    assert out.value > 0 and out.value % (64 * 4096 * 4) == 0
+    # fp32 partials of two or more K ranges, then one 8-byte arrival word per output tile
+    ranges, words = divmod(out.value, 64 * 4096 * 4)
+    assert ranges >= 2 and 0 < words <= 8 * 4096 and words % 8 == 0
     assert lib.ss_w4a16_workspace_size(64, 4096, 14336, 128, _ffi.SS_DTYPE_F32, ctypes.byref(out)) == _ffi.SS_OK
     assert out.value == 0  # fp32 activations take the scalar kernel
     st = lib.ss_w4a16_gemm(None, None, None, None, None, 0, 8, 256, 128, 256, 8, _ffi.SS_DTYPE_BF16,

@@ -165,6 +165,45 @@ def test_tiled_split_k(device, m, k, n, g, act, sdt):
     assert torch.equal(y, w4a16_gemm(xd, qd, sd, zd, g))  # repeat: bit-identical
 
 
+@pytest.mark.parametrize("m,n", [(48, 16512), (24, 16384)])
+def test_tiled_two_ranges_finished_in_kernel(device, m, n):
+    """Two K ranges at m <= 64 (K 2048; N 16512: 129 weight tiles, a 264-workgroup grid of
+    four waves; N 16384 at m 24: 256 workgroups of eight): the last range to arrive at a
+    tile adds both partials, counted in arrival words behind the partials in the workspace,
+    tagged per call. Correct on a workspace full of 0xFF bytes (no word carries the call's
+    tag), bit-identical across repeats, and a captured graph (one tag for every replay)
+    replays to the eager result with eager calls in between."""
+    from slipstream_amd.kernels import quant_gemm
+    print(f"w4a16 two-range tiled m={m} n={n}", flush=True)
+    x, qw, s, z, ref = _host_case(n, 2048, m, 128, seed=m + n, zeros="random")
+    xd, qd, sd, zd = x.to(device), qw.to(device), s.to(device), z.to(device)
+    y = w4a16_gemm(xd, qd, sd, zd, 128)
+    _assert_close(y, ref, f"two ranges m={m} n={n}")
+    torch.cuda.synchronize()
+    for ws in quant_gemm._WORKSPACE.values():
+        ws.fill_(0xFF)
+    y1 = w4a16_gemm(xd, qd, sd, zd, 128)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        w4a16_gemm(xd, qd, sd, zd, 128)
+    st.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        out = w4a16_gemm(xd, qd, sd, zd, 128)
+    for rep in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y), f"replay {rep}"
+        again = w4a16_gemm(xd, qd, sd, zd, 128)  # eager call between replays
+        torch.cuda.synchronize()
+        assert torch.equal(again, y)
+
+
 def test_tiled_uneven_ranges_from_the_table_cap(device):
     """K = 15360 at M = 40 over 258 weight tiles: one range per tile would need a 122 KB
     scale table, so the host splits K until a range's table fits 40 KB -- 4 ranges of 32,
