@@ -218,7 +218,7 @@ int ss_paged_attention_shared_prefix(const void* q, void* out, const void* k_cac
  * bandwidth GEMV; m >= 2 with group_size % 128 == 0: a tiled kernel that may
  * split K over workgroups); everything else a scalar fp32 kernel. The result
  * does not depend on timing: split-K partials are added in range order, by a
- * second kernel or (two ranges, m <= 64) by the last range of each output tile
+ * second kernel or (two ranges, n % 4 == 0) by the last range of each output tile
  * to finish, which a device-scope compare-and-swap on a tagged arrival word in
  * the workspace identifies; never by atomic adds.
  * workspace: ss_w4a16_workspace_size() reports the bytes of the split-K

@@ -490,8 +490,8 @@ __global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
 // rows each, every wave against all 16*MT activation rows) over one range of `kchunk`
 // 128-key stages. With several ranges (split K) each writes fp32 partials
 // part[z][m][n]; w4a16_splitk_reduce_kernel adds them in range order, or, with arrival
-// words (two ranges at m <= 64), the last range of each output tile to finish adds them
-// itself in the same order, so the result does not depend on timing.
+// words (two ranges), the last range of each output tile to finish adds the other's
+// partials to its own in the same order, so the result does not depend on timing.
 //   - Once per workgroup: the scale table of its rows and range, as pairs
 //     (s, s * (MAGIC + z)) in LDS (dynamic shared memory). Per-stage scale loads
 //     from memory, 16 scattered words per instruction, took the memory pipeline
@@ -726,9 +726,16 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
   static_assert(MTP >= 1, "a 16-row tile of results fits the activation stages");
   float* const s_t = reinterpret_cast<float*>(&s_x[0][0][0]);
   const bool split = ks > 1;
-  // with arrival words the last range finishes the tile (below); without, a second
-  // kernel adds the partials after this one
-  const bool fused = split && arrivals != nullptr;
+  // with arrival words (two ranges, N % 4 == 0) the last range finishes the tile (below);
+  // without, a second kernel adds the partials after this one
+  const bool fused = ks == 2 && arrivals != nullptr;
+  // 16-byte chunks (four columns of a row) of the tile per thread, per pass and in all:
+  // in pass P a thread handles the chunks P * CPP + li of its CPT (chunk i of a thread is
+  // q = threadIdx.x + NTHR i of the tile, rows of TW / 4 chunks)
+  constexpr int CPP = MTP * NS;
+  constexpr int CPT = MT * NS;
+  static_assert(MT % MTP == 0 && CPP * NTHR * 4 == MTP * 16 * TW, "passes of whole chunks per thread");
+  f32x4 own[CPT];  // this range's partial sums of the thread's chunks (the two-range finish)
   const bool vec_n = p.n % 4 == 0;
   const bool vec_out = vec_n && p.o_stride % 4 == 0 && ((uintptr_t)p.out & 7) == 0;
   // this range's partials: rows [m0, m0 + BM) of range zr, through a descriptor over
@@ -747,11 +754,14 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
         for (int e = 0; e < 4; ++e)
           s_t[(16 * (mt - mt0) + 4 * kg + e) * TROW + wave * 16 * NS + 16 * ns + ln] = acc[mt][ns][e];
     __syncthreads();
-    for (int q = threadIdx.x; q < MTP * 16 * (TW / 4); q += NTHR) {
+#pragma unroll
+    for (int li = 0; li < CPP; ++li) {
+      const int q = threadIdx.x + NTHR * li;
       const int rl = q / (TW / 4), c4 = q - rl * (TW / 4);
       const int m = m0 + 16 * mt0 + rl, n = nb + 4 * c4;
-      if (m >= p.m || n >= p.n) continue;
       const f32x4 v = *reinterpret_cast<const f32x4*>(&s_t[rl * TROW + 4 * c4]);
+      own[(mt0 / MTP) * CPP + li] = v;
+      if (m >= p.m || n >= p.n) continue;
       if (split && vec_n) {
         const int off = (int)(((int64_t)(m - m0) * p.n + n) * 4);
         if (fused)
@@ -777,49 +787,26 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
   }
   if (!fused) return;
 
-  // K split: the last of the tile's ranges to arrive adds every range's partials in
-  // range order ((0 + p0) + p1 + ...: the same sums in the same order whichever range
-  // arrives last) and writes the output, so no second launch is needed
+  // Two ranges: the last of the tile's two ranges to arrive adds the other's partials to
+  // its own (kept in registers) as (0 + p0) + p1 -- the reduce kernel's sums in its order,
+  // whichever range arrives last -- and writes the output: one batch of device-scope
+  // loads, half the tile's partial bytes, and no second launch
   __shared__ int s_last;
   wait_vm0();        // this thread's partials have reached the point of device coherence
   __syncthreads();   // every thread's, before the count moves
   if (threadIdx.x == 0) s_last = arrive_last(arrivals + (pair / ks) * m_blocks + (within >> 3), tag, ks) ? 1 : 0;
   __syncthreads();
   if (!s_last) return;
-  // each thread owns CPT 16-byte chunks (four columns of a row) of the BM x TW tile; the
-  // loads of range z + 1 are requested before range z is added (one memory round trip
-  // for the whole gather, not one per range)
-  constexpr int CPT = BM * TW / 4 / NTHR;
-  static_assert(CPT * NTHR * 4 == BM * TW, "the tile splits into whole chunks per thread");
-  const __amdgpu_buffer_rsrc_t rall = buffer_rsrc(part, (uint32_t)((int64_t)ks * p.m * p.n * 4));
-  int coff[CPT];  // byte offset of the chunk in range 0, or past every range (zeros)
+  float* const obase = part + ((int64_t)(1 - zr) * p.m + m0) * p.n;  // the other range's rows
+  const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(obase, (uint32_t)((int64_t)rows * p.n * 4));
+  u32x4 other[CPT];
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int q = threadIdx.x + NTHR * i;
     const int rl = q / (TW / 4), c4 = q - rl * (TW / 4);
     const int m = m0 + rl, n = nb + 4 * c4;
-    coff[i] = (m < p.m && n < p.n) ? (int)(((int64_t)m * p.n + n) * 4) : kOutOfRange;
-  }
-  const int zstride = (int)((int64_t)p.m * p.n * 4);
-  auto gather = [&](int z, u32x4 (&v)[CPT]) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i)
-      v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                           rall, coff[i], z < ks ? z * zstride : kOutOfRange, kDeviceScope));
-  };
-  f32x4 y[CPT];
-#pragma unroll
-  for (int i = 0; i < CPT; ++i) y[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  u32x4 vcur[CPT], vnext[CPT];
-  gather(0, vcur);
-  for (int z = 0; z < ks; ++z) {
-    gather(z + 1, vnext);
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const f32x4 v = __builtin_bit_cast(f32x4, vcur[i]);
-      y[i][0] += v[0], y[i][1] += v[1], y[i][2] += v[2], y[i][3] += v[3];
-      vcur[i] = vnext[i];
-    }
+    const int off = (m < p.m && n < p.n) ? (int)(((int64_t)rl * p.n + n) * 4) : kOutOfRange;
+    other[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, off, 0, kDeviceScope));
   }
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
@@ -827,14 +814,19 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const int rl = q / (TW / 4), c4 = q - rl * (TW / 4);
     const int m = m0 + rl, n = nb + 4 * c4;
     if (m >= p.m || n >= p.n) continue;
+    const f32x4 po = __builtin_bit_cast(f32x4, other[i]);
+    const f32x4 p0 = zr == 0 ? own[i] : po, p1 = zr == 0 ? po : own[i];
+    f32x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = (0.f + p0[e]) + p1[e];
     T* const o = (T*)p.out + (int64_t)m * p.o_stride + n;
     if (vec_out) {
-      const T h[4] = {(T)y[i][0], (T)y[i][1], (T)y[i][2], (T)y[i][3]};
+      const T h[4] = {(T)y[0], (T)y[1], (T)y[2], (T)y[3]};
       *reinterpret_cast<u32x2*>(o) = __builtin_bit_cast(u32x2, h);
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (n + e < p.n) o[e] = (T)y[i][e];
+        if (n + e < p.n) o[e] = (T)y[e];
     }
   }
 }
@@ -1655,11 +1647,12 @@ int launch_w4a16_tile(const W4Params& p, const W4Plan& pl, float* part, hipStrea
     ss_host::set_error("w4a16 gemm: %lld tiled workgroups", (long long)grid);
     return SS_ERR_UNSUPPORTED;
   }
-  // Two ranges at m <= 64: the last range of each tile adds the two partials itself (C5
-  // gate and gate_up at m = 32 and 64: 7-9 % faster than a second kernel). With more
-  // ranges, or 64-row blocks of m = 256, that last workgroup's gather outlasts a reduce
+  // Two ranges (and whole 16-byte row chunks, N % 4 == 0): the last range of each tile
+  // adds the other range's partials to its own itself (C5 gate and gate_up at m = 32 and
+  // 64: 7-9 % faster than a second kernel; at m = 256 gate 51.2 against 54.2 us, gate_up
+  // 100.6 against 103.5). With more ranges that last workgroup's gather outlasts a reduce
   // kernel spread over the whole GPU (o at m = 64, 8 ranges: 21.4 against 16.4 us).
-  const bool fused = pl.ks == 2 && p.m <= 64;
+  const bool fused = pl.ks == 2 && p.n % 4 == 0;
   unsigned long long* const arrivals = fused ? (unsigned long long*)((char*)part + tile_part_bytes(pl, p.m, p.n)) : nullptr;
   const unsigned long long tag = fused ? next_arrival_tag() : 0ull;
   hipLaunchKernelGGL((w4a16_tile_kernel<T, MT, NS, PF, WV>), dim3((unsigned)grid), dim3(64 * WV), pl.lds, stream, p,

@@ -165,11 +165,13 @@ def test_tiled_split_k(device, m, k, n, g, act, sdt):
     assert torch.equal(y, w4a16_gemm(xd, qd, sd, zd, g))  # repeat: bit-identical
 
 
-@pytest.mark.parametrize("m,n", [(48, 16512), (24, 16384)])
+@pytest.mark.parametrize("m,n", [(48, 16512), (24, 16384), (130, 16512)])
 def test_tiled_two_ranges_finished_in_kernel(device, m, n):
-    """Two K ranges at m <= 64 (K 2048; N 16512: 129 weight tiles, a 264-workgroup grid of
-    four waves; N 16384 at m 24: 256 workgroups of eight): the last range to arrive at a
-    tile adds both partials, counted in arrival words behind the partials in the workspace,
+    """Two K ranges (K 2048; N 16512 at m 48: 129 weight tiles, a 264-workgroup grid of
+    four waves; N 16384 at m 24: 256 workgroups of eight; N 16512 at m 130: 65 tiles of 256
+    rows, the last half full, in three 64-row blocks, the last of 2 rows): the last range to
+    arrive at a tile adds the other range's partials to its own (kept in registers),
+    counted in arrival words behind the partials in the workspace,
     tagged per call. Correct on a workspace full of 0xFF bytes (no word carries the call's
     tag), bit-identical across repeats, and a captured graph (one tag for every replay)
     replays to the eager result with eager calls in between."""
