@@ -1649,8 +1649,8 @@ int launch_w4a16_tile(const W4Params& p, const W4Plan& pl, float* part, hipStrea
   }
   // Two ranges (and whole 16-byte row chunks, N % 4 == 0): the last range of each tile
   // adds the other range's partials to its own itself (C5 gate and gate_up at m = 32 and
-  // 64: 7-9 % faster than a second kernel; at m = 256 gate 51.2 against 54.2 us, gate_up
-  // 100.6 against 103.5). With more ranges that last workgroup's gather outlasts a reduce
+  // 64: 7-9 % faster than a second kernel; at m = 256 gate 51.4 against 54.8 us, gate_up
+  // 99.3 against 101.2). With more ranges that last workgroup's gather outlasts a reduce
   // kernel spread over the whole GPU (o at m = 64, 8 ranges: 21.4 against 16.4 us).
   const bool fused = pl.ks == 2 && p.n % 4 == 0;
   unsigned long long* const arrivals = fused ? (unsigned long long*)((char*)part + tile_part_bytes(pl, p.m, p.n)) : nullptr;
