@@ -1409,16 +1409,18 @@ struct W4Plan {
 // rounds. Shapes (activation tiles MT, weight tiles NS per wave, prefetch depth PF)
 // by m: the bandwidth-bound sizes keep eight stages of weights in flight per wave;
 // m > 64 takes 64 x 64 wave tiles. The K split aims at one workgroup
-// per CU for m <= 64 (the nearest whole count of ranges: 224 weight tiles stay
-// unsplit) and two for m > 64 (at least that many), in ranges of equal length (the
-// split count divides the rounds of PF stages), with the workgroup's scale table within
+// per CU for m <= 64 and two for m > 64 (the nearest whole count of ranges: 224
+// weight tiles at m <= 64 stay unsplit), in ranges of equal length (the split count
+// divides the rounds of PF stages), with the workgroup's scale table within
 // kTileTableMax bytes of LDS; the partials take ks * m * n floats of workspace.
 // Measured over the Llama-3-8B linears (kernel + reduce), e.g. 4096 x 6144 at
 // m = 64: 19.9 us for 4 ranges against 22.9 us for 8 and 22.7 us for 3 uneven
 // ones; 4096 x 28672 at m = 64: 39.9 us unsplit against 46.6 us for 3 ranges;
 // 14336 x 4096 at m = 256: 56.4 us for 8 ranges against 66.0 us for 4; 4096 x 28672
 // (224 tiles) at m = 32 / 64: 23.2 / 33.1 us unsplit against 26.8 / 34.3 us for two
-// ranges finished in-kernel. The
+// ranges finished in-kernel; at m = 192 rounding to the nearest count rather than up
+// takes 4096 x 6144 from 8 ranges to 4 (37.1 -> 35.8 us) and 4096 x 14336 from 4 to 2
+// (52.9 -> 51.2 us). The
 // table cap keeps two workgroups per CU: with the 35 KB activation stages of
 // m > 32, a 64 KB table left room for one (a 4096 x 28672 linear at m = 256 took
 // 233 us instead of 2 x 67 us).
@@ -1453,7 +1455,7 @@ bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
   const int64_t target = (m <= 64 ? 1LL : 2LL) * ss_host::device_cu_count();
   const int64_t tiles = n_tiles * m_blocks;
   const int64_t rounds = iters / pf;
-  int64_t ks = m <= 64 ? (target + tiles / 2) / tiles : (target + tiles - 1) / tiles;
+  int64_t ks = (target + tiles / 2) / tiles;
   ks = ks < 1 ? 1 : (ks > rounds ? rounds : ks);
   while (ks > 1 && rounds % ks) --ks;  // equal ranges
   if (ks > 65535) return false;
