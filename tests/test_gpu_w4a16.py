@@ -165,22 +165,27 @@ def test_tiled_split_k(device, m, k, n, g, act, sdt):
     assert torch.equal(y, w4a16_gemm(xd, qd, sd, zd, g))  # repeat: bit-identical
 
 
-@pytest.mark.parametrize("m,n", [(48, 16512), (24, 16384), (130, 16512)])
-def test_tiled_two_ranges_finished_in_kernel(device, m, n):
+@pytest.mark.parametrize("m,n,act,sdt", [(48, 16512, torch.bfloat16, torch.float16),
+                                         (24, 16384, torch.bfloat16, torch.float16),
+                                         (130, 16512, torch.bfloat16, torch.float16),
+                                         (40, 16400, torch.float16, torch.bfloat16)])
+def test_tiled_two_ranges_finished_in_kernel(device, m, n, act, sdt):
     """Two K ranges (K 2048; N 16512 at m 48: 129 weight tiles, a 264-workgroup grid of
     four waves; N 16384 at m 24: 256 workgroups of eight; N 16512 at m 130: 65 tiles of 256
-    rows, the last half full, in three 64-row blocks, the last of 2 rows): the last range to
+    rows, the last half full, in three 64-row blocks, the last of 2 rows; N 16400 at m 40:
+    fp16 activations and bf16 scales, a last weight tile of 16 rows): the last range to
     arrive at a tile adds the other range's partials to its own (kept in registers),
     counted in arrival words behind the partials in the workspace,
     tagged per call. Correct on a workspace full of 0xFF bytes (no word carries the call's
     tag), bit-identical across repeats, and a captured graph (one tag for every replay)
     replays to the eager result with eager calls in between."""
     from slipstream_amd.kernels import quant_gemm
-    print(f"w4a16 two-range tiled m={m} n={n}", flush=True)
-    x, qw, s, z, ref = _host_case(n, 2048, m, 128, seed=m + n, zeros="random")
+    print(f"w4a16 two-range tiled m={m} n={n} {act}", flush=True)
+    x, qw, s, z, ref = _host_case(n, 2048, m, 128, seed=m + n, act=act, sdt=sdt, zeros="random")
     xd, qd, sd, zd = x.to(device), qw.to(device), s.to(device), z.to(device)
     y = w4a16_gemm(xd, qd, sd, zd, 128)
-    _assert_close(y, ref, f"two ranges m={m} n={n}")
+    assert y.dtype == act
+    _assert_close(y, ref, f"two ranges m={m} n={n} {act}")
     torch.cuda.synchronize()
     for ws in quant_gemm._WORKSPACE.values():
         ws.fill_(0xFF)
