@@ -1407,8 +1407,11 @@ struct W4Plan {
 
 // Tiled kernel for m >= 2 when g % 128 == 0 and K is a whole number of PF-stage
 // rounds. Shapes (activation tiles MT, weight tiles NS per wave, prefetch depth PF)
-// by m: the bandwidth-bound sizes keep eight stages of weights in flight per wave;
-// m > 64 takes 64 x 64 wave tiles. The K split aims at one workgroup
+// by m: two stages of weights in flight per wave everywhere (at m = 32 against eight:
+// 4096 x 6144 12.2 vs 14.2 us, 14336 x 4096 17.0 vs 19.5 us; at m = 48 / 64 against
+// four: 16.5 vs 17.3 us, 4096 x 4096 15.9 vs 16.5 us at m = 64; a shallower ring also
+// gives the K split more rounds to divide); m > 64 takes 64 x 64 wave tiles. The K
+// split aims at one workgroup
 // per CU for m <= 64 and two for m > 64 (the nearest whole count of ranges: 224
 // weight tiles at m <= 64 stay unsplit), in ranges of equal length (the split count
 // divides the rounds of PF stages), with the workgroup's scale table within
@@ -1440,11 +1443,11 @@ bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
   if (m <= 16 && k < 8192 && n < 24576) return false;
   int mt, ns, pf;
   if (m <= 16)
-    mt = 1, ns = 2, pf = 8;
+    mt = 1, ns = 2, pf = 2;
   else if (m <= 32)
-    mt = 2, ns = 2, pf = 8;
+    mt = 2, ns = 2, pf = 2;
   else if (m <= 64)
-    mt = 4, ns = 2, pf = 4;
+    mt = 4, ns = 2, pf = 2;
   else
     mt = 4, ns = 4, pf = 2;
   const int64_t iters = k / 128;
@@ -1778,13 +1781,13 @@ int launch_w4a16_typed(const W4Params& p, const W4Plan& pl, float* part, hipStre
     // m = 32 and 64 took 11-17 % longer with eight, m = 256 3-10 %).
     const int64_t grid = ((int64_t)pl.ks * pl.n_tiles + 7) / 8 * 8 * pl.m_blocks;
     const bool eight = grid <= ss_host::device_cu_count();
-    if (pl.mt == 1) return launch_w4a16_tile<T, 1, 2, 8, 4>(p, pl, part, stream);
+    if (pl.mt == 1) return launch_w4a16_tile<T, 1, 2, 2, 4>(p, pl, part, stream);
     if (pl.mt == 2)
-      return eight ? launch_w4a16_tile<T, 2, 1, 8, 8>(p, pl, part, stream)
-                   : launch_w4a16_tile<T, 2, 2, 8, 4>(p, pl, part, stream);
+      return eight ? launch_w4a16_tile<T, 2, 1, 2, 8>(p, pl, part, stream)
+                   : launch_w4a16_tile<T, 2, 2, 2, 4>(p, pl, part, stream);
     if (pl.ns == 2)
-      return eight ? launch_w4a16_tile<T, 4, 1, 4, 8>(p, pl, part, stream)
-                   : launch_w4a16_tile<T, 4, 2, 4, 4>(p, pl, part, stream);
+      return eight ? launch_w4a16_tile<T, 4, 1, 2, 8>(p, pl, part, stream)
+                   : launch_w4a16_tile<T, 4, 2, 2, 4>(p, pl, part, stream);
     return launch_w4a16_tile<T, 4, 4, 2, 4>(p, pl, part, stream);
   }
   if (pl.gemv) {
