@@ -1681,8 +1681,10 @@ int launch_w4a16_tile(const W4Params& p, const W4Plan& pl, float* part, hipStrea
 
 template <typename T, int MT, int NS, int ST>
 int launch_w4a16_skinny_st(const W4Params& p, const W4Plan& pl, hipStream_t stream) {
-  // stages in flight: four, or two where four would not fit the registers (eight stages
-  // of four weight tiles; eight stages under the 128 registers of 16-wave workgroups)
+  // stages in flight: two, or four for four weight tiles of fewer than eight stages
+  // (A B B A at m = 5..16: two against four, 4096 x 4096 5.05 vs 5.50 us at m = 5, 5.25
+  // vs 5.61 at m = 8, 4096 x 6144 7.24 vs 7.38 at m = 8; four tiles of 4096 x 14336 12.2
+  // vs 11.7 us at m = 5 with two)
   constexpr int P4 = 4 < ST ? 4 : ST;
   constexpr int P2 = 2 < ST ? 2 : ST;
   // 16-wave workgroups get 128 registers a lane; up to 8 waves, 256
@@ -1705,7 +1707,7 @@ int launch_w4a16_skinny_st(const W4Params& p, const W4Plan& pl, hipStream_t stre
     ss_host::set_error("w4a16 gemm: skinny plan with %d waves and %d weight tiles", pl.kw, NS);
     return SS_ERR_UNSUPPORTED;
   }
-  return launch(w4a16_skinny_kernel<T, MT, NS, ST, NS >= 4 && ST >= 8 ? P2 : P4, 512>);
+  return launch(w4a16_skinny_kernel<T, MT, NS, ST, NS >= 4 && ST < 8 ? P4 : P2, 512>);
 }
 
 template <typename T, int MT>
