@@ -505,7 +505,8 @@ __global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
 //     end of the buffer: they return zeros without touching memory, and the loop
 //     needs no branch.
 //   - The loop is VALU-bound rather than MFMA- or memory-bound: per stage and wave
-//     (MT = NS = 4) 64 MFMAs against about 300 VALU instructions -- the nibble
+//     (MT = NS = 4, the m > 64 tiles when this was measured) 64 MFMAs against about
+//     300 VALU instructions -- the nibble
 //     unpack (8 per 32-bit word), the fold (2 FMAs per accumulator element) and the
 //     activation staging (its row sums as v_dot2 against ones: 48 fewer per stage
 //     than converting and adding each value, 124.6 -> 118.5 us for the C5 layer at
@@ -1410,7 +1411,9 @@ struct W4Plan {
 // by m: two stages of weights in flight per wave everywhere (at m = 32 against eight:
 // 4096 x 6144 12.2 vs 14.2 us, 14336 x 4096 17.0 vs 19.5 us; at m = 48 / 64 against
 // four: 16.5 vs 17.3 us, 4096 x 4096 15.9 vs 16.5 us at m = 64; a shallower ring also
-// gives the K split more rounds to divide); m > 64 takes 64 x 64 wave tiles. The K
+// gives the K split more rounds to divide); m > 32 takes 64 x 32 wave tiles (at m = 128
+// / 256 against 64 x 64: 4096 x 6144 25.5 / 30.0 vs 28.5 / 36.5 us, 4096 x 14336 31.5 /
+// 50.0 vs 37.4 / 51.6 us, 4096 x 28672 52.4 / 96.3 vs 54.8 / 100.4 us). The K
 // split aims at one workgroup
 // per CU for m <= 64 and two for m > 64 (the nearest whole count of ranges: 224
 // weight tiles at m <= 64 stay unsplit), in ranges of equal length (the split count
@@ -1446,10 +1449,8 @@ bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
     mt = 1, ns = 2, pf = 2;
   else if (m <= 32)
     mt = 2, ns = 2, pf = 2;
-  else if (m <= 64)
-    mt = 4, ns = 2, pf = 2;
   else
-    mt = 4, ns = 4, pf = 2;
+    mt = 4, ns = 2, pf = 2;
   const int64_t iters = k / 128;
   if (iters % pf) return false;
   const int64_t n_tiles = (n + 64 * ns - 1) / (64 * ns);
@@ -1787,10 +1788,8 @@ int launch_w4a16_typed(const W4Params& p, const W4Plan& pl, float* part, hipStre
     if (pl.mt == 2)
       return eight ? launch_w4a16_tile<T, 2, 1, 2, 8>(p, pl, part, stream)
                    : launch_w4a16_tile<T, 2, 2, 2, 4>(p, pl, part, stream);
-    if (pl.ns == 2)
-      return eight ? launch_w4a16_tile<T, 4, 1, 2, 8>(p, pl, part, stream)
-                   : launch_w4a16_tile<T, 4, 2, 2, 4>(p, pl, part, stream);
-    return launch_w4a16_tile<T, 4, 4, 2, 4>(p, pl, part, stream);
+    return eight ? launch_w4a16_tile<T, 4, 1, 2, 8>(p, pl, part, stream)
+                 : launch_w4a16_tile<T, 4, 2, 2, 4>(p, pl, part, stream);
   }
   if (pl.gemv) {
     if (p.k <= 8192)

@@ -144,9 +144,9 @@ def test_batch1_gemv_strided_activation(device):
 # (plans as the host computes them for 256 CUs: ranges x stages, weight tiles, M blocks)
 @pytest.mark.parametrize("m,k,n,g,act,sdt", [
     (50, 3072, 12750, 128, torch.bfloat16, torch.float16),   # 3 ranges of 8 stages; 100 tiles: 300 pairs, 4 padding ids
-    (33, 3584, 2000, 896, torch.float16, torch.bfloat16),    # 7 ranges of 4 stages: groups of 7 stages straddle them
-    (100, 4096, 1000, 256, torch.bfloat16, torch.float32),   # 64x64 wave tiles, a partial second M block
-    (130, 1792, 700, 128, torch.bfloat16, torch.float16),    # 3 M blocks of one weight tile on one XCD; 21 pairs
+    (33, 3584, 2000, 896, torch.float16, torch.bfloat16),    # 14 ranges of 2 stages: groups of 7 stages straddle them
+    (100, 4096, 1000, 256, torch.bfloat16, torch.float32),   # 64x32 wave tiles, a partial second M block
+    (130, 1792, 700, 128, torch.bfloat16, torch.float16),    # 3 M blocks of one weight tile on one XCD; 42 pairs
     (24, 8192, 3000, 512, torch.float16, torch.float16),     # 32-row activation tiles
     (9, 8192, 700, 256, torch.bfloat16, torch.bfloat16),     # m <= 16, g 256 (the skinny kernel takes only g 128)
     (16, 1024, 24600, 256, torch.bfloat16, torch.float16),   # m <= 16 at N >= 24576, unsplit, 193 tiles
@@ -167,11 +167,11 @@ def test_tiled_split_k(device, m, k, n, g, act, sdt):
 
 @pytest.mark.parametrize("m,n,act,sdt", [(48, 16512, torch.bfloat16, torch.float16),
                                          (24, 16384, torch.bfloat16, torch.float16),
-                                         (130, 16512, torch.bfloat16, torch.float16),
+                                         (130, 12352, torch.bfloat16, torch.float16),
                                          (40, 16400, torch.float16, torch.bfloat16)])
 def test_tiled_two_ranges_finished_in_kernel(device, m, n, act, sdt):
     """Two K ranges (K 2048; N 16512 at m 48: 129 weight tiles, a 264-workgroup grid of
-    four waves; N 16384 at m 24: 256 workgroups of eight; N 16512 at m 130: 65 tiles of 256
+    four waves; N 16384 at m 24: 256 workgroups of eight; N 12352 at m 130: 97 tiles of 128
     rows, the last half full, in three 64-row blocks, the last of 2 rows; N 16400 at m 40:
     fp16 activations and bf16 scales, a last weight tile of 16 rows): the last range to
     arrive at a tile adds the other range's partials to its own (kept in registers),
