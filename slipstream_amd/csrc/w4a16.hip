@@ -1451,6 +1451,11 @@ bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
     mt = 2, ns = 2, pf = 2;
   else
     mt = 4, ns = 2, pf = 2;
+  // small grids (64-row blocks x 128-row weight tiles at most half the CUs, K <= 8192):
+  // 32-row activation tiles, twice the workgroups before any K split (m = 64: 4096 x
+  // 6144 14.6 vs 17.8 us, 4096 x 4096 12.7 vs 15.8, 4096 x 14336 20.4 vs 22.4; m = 256:
+  // 4096 x 4096 21.6 vs 26.9 us); with larger K (14336 x 4096) or grids they are slower
+  if (mt == 4 && k <= 8192 && ((n + 127) / 128) * ((m + 63) / 64) <= ss_host::device_cu_count() / 2) mt = 2;
   const int64_t iters = k / 128;
   if (iters % pf) return false;
   const int64_t n_tiles = (n + 64 * ns - 1) / (64 * ns);

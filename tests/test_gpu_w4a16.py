@@ -143,16 +143,16 @@ def test_batch1_gemv_strided_activation(device):
 
 # (plans as the host computes them for 256 CUs: ranges x stages, weight tiles, M blocks)
 @pytest.mark.parametrize("m,k,n,g,act,sdt", [
-    (50, 3072, 12750, 128, torch.bfloat16, torch.float16),   # 3 ranges of 8 stages; 100 tiles: 300 pairs, 4 padding ids
-    (33, 3584, 2000, 896, torch.float16, torch.bfloat16),    # 14 ranges of 2 stages: groups of 7 stages straddle them
-    (100, 4096, 1000, 256, torch.bfloat16, torch.float32),   # 64x32 wave tiles, a partial second M block
-    (130, 1792, 700, 128, torch.bfloat16, torch.float16),    # 3 M blocks of one weight tile on one XCD; 42 pairs
+    (50, 3072, 12750, 128, torch.bfloat16, torch.float16),   # 32-row tiles, 2 M blocks, one range; 100 tiles: 4 padding ids
+    (33, 3584, 2000, 896, torch.float16, torch.bfloat16),    # 7 ranges of 4 stages: groups of 7 stages straddle them
+    (100, 4096, 1000, 256, torch.bfloat16, torch.float32),   # 32-row tiles (small grid), a partial fourth M block, 16 ranges
+    (130, 1792, 700, 128, torch.bfloat16, torch.float16),    # 5 M blocks of one weight tile on one XCD; 42 pairs
     (24, 8192, 3000, 512, torch.float16, torch.float16),     # 32-row activation tiles
     (9, 8192, 700, 256, torch.bfloat16, torch.bfloat16),     # m <= 16, g 256 (the skinny kernel takes only g 128)
     (16, 1024, 24600, 256, torch.bfloat16, torch.float16),   # m <= 16 at N >= 24576, unsplit, 193 tiles
     (24, 2048, 3000, 128, torch.bfloat16, torch.float16),    # 32-row tiles, grid within the CUs: eight waves
     (32, 4096, 20480, 128, torch.bfloat16, torch.float16),   # 32-row tiles, 2 ranges, 320 workgroups: four waves
-    (64, 2048, 8000, 128, torch.float16, torch.bfloat16),    # 64-row tiles, grid within the CUs: eight waves
+    (64, 2048, 8000, 128, torch.float16, torch.bfloat16),    # 32-row tiles, 2 ranges, grid within the CUs: eight waves
 ])
 def test_tiled_split_k(device, m, k, n, g, act, sdt):
     """The tiled kernel (activations shared through LDS, K split over workgroups with
