@@ -1455,13 +1455,18 @@ bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
   // 32-row activation tiles, twice the workgroups before any K split (m = 64: 4096 x
   // 6144 14.6 vs 17.8 us, 4096 x 4096 12.7 vs 15.8, 4096 x 14336 20.4 vs 22.4; m = 256:
   // 4096 x 4096 21.6 vs 26.9 us); with larger K (14336 x 4096) or grids they are slower
-  if (mt == 4 && k <= 8192 && ((n + 127) / 128) * ((m + 63) / 64) <= ss_host::device_cu_count() / 2) mt = 2;
+  const bool small_grid =
+      mt == 4 && k <= 8192 && ((n + 127) / 128) * ((m + 63) / 64) <= ss_host::device_cu_count() / 2;
+  if (small_grid) mt = 2;
   const int64_t iters = k / 128;
   if (iters % pf) return false;
   const int64_t n_tiles = (n + 64 * ns - 1) / (64 * ns);
   const int64_t m_blocks = (m + 16 * mt - 1) / (16 * mt);
   if (n_tiles > 65535 || m_blocks > 65535) return false;
-  const int64_t target = (m <= 64 ? 1LL : 2LL) * ss_host::device_cu_count();
+  // one workgroup per CU at m <= 64 and on small grids, two otherwise (m = 128: 4096 x
+  // 4096 15.7 vs 18.1 us, 4096 x 6144 19.7 vs 21.2 with one; 14336 x 4096 at m = 256
+  // 52.5 with two against 61.1 with one)
+  const int64_t target = (m <= 64 || small_grid ? 1LL : 2LL) * ss_host::device_cu_count();
   const int64_t tiles = n_tiles * m_blocks;
   const int64_t rounds = iters / pf;
   int64_t ks = (target + tiles / 2) / tiles;
