@@ -153,8 +153,11 @@ int ss_paged_attention_varlen_noalloc(const void* q, void* out, const void* k_ca
  *     KV tokens than the shared prefix; its suffix counted as empty (it attended the
  *     whole prefix).
  * The reference raises ValueError at such inputs (slipstream/models/layers/attention.py:44-45);
- * a device kernel cannot, so it writes defined values and reports here. Waits for
- * `stream`, then stores the word in *flags and clears it when `clear` is nonzero.
+ * a device kernel cannot, so it writes defined values and reports here. Reads the
+ * word on `stream` (after the work queued there), stores it in *flags and, when `clear`
+ * is nonzero, clears it in the same atomic exchange, so no bit is lost to a race with
+ * kernels on other streams; bits of work still running on other streams appear in a
+ * later read.
  * No counterpart in the reference (its checks are synchronous host code).
  */
 #define SS_STATUS_QUERY_TOO_LONG 1

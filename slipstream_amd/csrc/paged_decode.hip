@@ -39,6 +39,14 @@ __device__ __attribute__((aligned(16))) uint32_t g_zero_row[128];
 // Device status word of this GPU (kStatus* bits), read and cleared by
 // ss_attention_status. Kernels only OR bits into it.
 __device__ int g_status;
+// The word as status_take_kernel last read it.
+__device__ int g_status_seen;
+
+// One thread: take the status word (exchange with 0 when clearing, else read it
+// through an atomic that changes nothing) and leave it where the host copies it from.
+__global__ void status_take_kernel(int clear) {
+  g_status_seen = clear ? atomicExch(&g_status, 0) : atomicOr(&g_status, 0);
+}
 
 __device__ __forceinline__ int block_sum(int v, int* sh) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -774,12 +782,16 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const AttnParams p, i
     if (p.px_n > 0 && c0 >= 0) {
       // shared-prefix cascade: the sequences this range finished (one query token
       // each), completed with the prefix parts; one thread per (sequence, query head
-      // of the head group, 8 consecutive d)
+      // of the head group, 8 consecutive d). [c0, c1) spans the first and last
+      // sequence the range finished; a sequence between them with no suffix pair
+      // (seq_len == prefix tokens) was skipped by the walker, left no state here, and
+      // is written by its own per-sequence block from the prefix parts alone.
       constexpr int DV = D / 8;
       const int hrows = p.hpw * p.n_rep;
       for (int u = tid; u < (c1 - c0) * hrows * DV; u += blockDim.x) {
         const int c = u % DV, t = u / DV;
         const int bb = c0 + t / hrows, hq = hg * hrows + t % hrows;
+        if (decode_pairs(p, bb) == 0) continue;
         const int64_t row = (int64_t)bb * p.n_q + hq;
         float m = p.px_seq_ml[row * 2], l = p.px_seq_ml[row * 2 + 1];
         const f32x4* po = reinterpret_cast<const f32x4*>(p.px_seq_o + row * D + 8 * c);
@@ -974,17 +986,17 @@ static int launch_decode_typed(AttnParams p, int max_query_len, char* ws, int64_
 }
 
 // Read (and optionally clear) this device's status word after the work queued on
-// `stream` has finished.
+// `stream` has finished. The read and the clear are one atomic exchange on the device,
+// so a bit that a kernel on another stream ORs in meanwhile is never erased unseen (it
+// is either in this read or still in the word for the next one); such a kernel's bits
+// show up only once it has run.
 int read_status(int* flags, int clear, hipStream_t stream) {
+  hipLaunchKernelGGL(status_take_kernel, dim3(1), dim3(1), 0, stream, clear);
+  if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
   if (hipStreamSynchronize(stream) != hipSuccess) return SS_ERR_LAUNCH;
   int v = 0;
-  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_status), sizeof(int), 0, hipMemcpyDeviceToHost) != hipSuccess)
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_status_seen), sizeof(int), 0, hipMemcpyDeviceToHost) != hipSuccess)
     return SS_ERR_LAUNCH;
-  if (clear && v != 0) {
-    const int zero = 0;
-    if (hipMemcpyToSymbol(HIP_SYMBOL(g_status), &zero, sizeof(int), 0, hipMemcpyHostToDevice) != hipSuccess)
-      return SS_ERR_LAUNCH;
-  }
   *flags = v;
   return SS_OK;
 }

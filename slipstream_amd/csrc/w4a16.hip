@@ -58,9 +58,11 @@ constexpr int kNonTemporal = 2;
 // device coherence, a load not served by possibly stale lines of this CU's or XCD's caches.
 constexpr int kDeviceScope = 16;
 
-// s_waitcnt vmcnt(0) with the other counters left alone (gfx9 encoding): every vector
-// memory operation of this wave, stores included, has completed
-__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8)); }
+// s_waitcnt vmcnt(0): every vector memory operation of this wave, stores included, has
+// completed. Inline asm with a memory clobber, so the compiler keeps every load and store
+// written before it on this side of the wait (the waitcnt builtin is not a memory
+// operation, and the stores it must cover could be sunk past it).
+__device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Arrival count of one output tile's K ranges in a 64-bit word: bits 8.. hold the call's
 // tag, bits 0..7 the ranges arrived. A word with another tag (an earlier call, or memory
@@ -70,7 +72,10 @@ __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt((0x7 << 
 // No cache maintenance: the partials are device-scope stores the caller has waited for
 // (vmcnt 0) before it arrives, the count is a device-scope atomic, and the last range
 // reads the partials with device-scope loads. (Release/acquire fences at device scope
-// write back or invalidate a whole L2 per wave, several times slower.)
+// write back or invalidate a whole L2 per wave, several times slower.) This relies on
+// sc1 stores reaching the point of device coherence before their vmcnt decrements, and
+// on sc1 loads not being served by this XCD's possibly stale L2 lines: the gfx950
+// memory model's meaning of the agent-scope cache policy bits.
 __device__ __forceinline__ bool arrive_last(unsigned long long* word, unsigned long long tag, int ranges) {
   unsigned long long old = 0ull;
   unsigned long long now;

@@ -153,4 +153,39 @@ def test_sequence_shorter_than_prefix_is_flagged(device, monkeypatch):
     assert attention_status(clear=True) & SS_STATUS_PREFIX_SHORT
     rows = [i for i in range(b.batch) if i != 5]
     assert_attn_close(out[rows], _oracle(b, rows), "rows that keep the promise")
-    assert torch.isfinite(out[5].float()).all()
+    # the flagged row: its suffix counts as empty, so it is attention over the whole
+    # shared prefix (the first shared_blocks entries of its own table)
+    kv = f64(b.kv_cache)
+    tables = tables_array([b.tables_host[5]], b.block_tables.shape[1])
+    ref5 = ora.paged_attention(f64(b.padded_q()[5:6]), kv, tables, np.array([b.shared_blocks * 16]), 0, b.scale,
+                               b.block_size)
+    assert_attn_close(out[5:6], ref5, "flagged row = prefix only")
+
+
+@pytest.mark.parametrize("n_kv", [8, 4])
+def test_empty_suffixes_between_short_ones(device, n_kv):
+    """Sequences with an empty suffix (seq_len == prefix tokens) sit between sequences of
+    one or two 32-key pairs, with one long suffix so that every decode range holds
+    several pairs: a range then finishes a run of short suffixes with empty ones inside
+    it. Every row is checked against the oracle, and the result repeats bit for bit
+    (no race between the range's merge block and an empty suffix's own block)."""
+    rng = np.random.default_rng(40 + n_kv)
+    prefix_blocks, batch = 20, 96
+    p_tok = prefix_blocks * 16
+    suffix = []
+    for i in range(batch):
+        suffix.append(0 if i % 2 else int(rng.integers(1, 65)))
+    suffix[37] = 7000
+    mk = lambda sfx, seed: workloads.build_batch(  # noqa: E731
+        [p_tok + s for s in sfx], [1] * batch, n_q=4 * n_kv, n_kv=n_kv, head_dim=128, block_size=16,
+        dtype=torch.bfloat16, device=device, seed=seed, pool_factor=1.3, shared_prefix_blocks=prefix_blocks)
+    # a call of the same shape whose odd rows have suffixes first: the workspace (same
+    # size, so the caching allocator hands the same block back) then holds finished-row
+    # state for the rows that are empty in the call under test
+    primed = mk([s if s else 40 for s in suffix], 90 + n_kv)
+    _run(primed, prefix_blocks)
+    b = mk(suffix, 3 + n_kv)
+    out = _run(b, prefix_blocks)
+    assert_attn_close(out, _oracle(b), f"empty suffixes between short ones, n_kv {n_kv}")
+    for _ in range(3):
+        assert torch.equal(out, _run(b, prefix_blocks))
