@@ -83,11 +83,18 @@ int ss_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_ca
  * out(b, t, h, d) = out + b*o_strides[0] + t*o_strides[1] + h*o_strides[2] + d
  * cache element (blk, off, h, d) = cache + blk*c_strides[0] + off*c_strides[1] + h*c_strides[2] + d
  * block_tables(b, i) = block_tables[b * bt_stride + i]
- * dtype: SS_DTYPE_BF16 or SS_DTYPE_F16 (q, cache and out share it).
+ * dtype: SS_DTYPE_BF16, SS_DTYPE_F16 or SS_DTYPE_F32 (q, cache and out share it);
+ * head_dim 1..256, block_size 1..1024 (the Triton decode's range, triton_paged.py:22-23,
+ * 283-284: head_dim <= 256, block_size <= 128, any float dtype). bf16 / fp16 at head_dim
+ * 64, 128 or 256 with power-of-two blocks of at least 4 tokens, 16-byte aligned planes
+ * and strides that are multiples of 8 elements take the MFMA decode and prefill
+ * kernels; every other call takes the general kernel (fp32 arithmetic, element strides).
  * workspace: device scratch of at least ss_paged_attention_workspace_size() bytes: the
  * split-K decode partials (sized by occupancy) and, when max_query_len * n_q / n_kv
  * exceeds 16 (prefill rows), the prefill work list (4 bytes per sequence and
- * 128-row query tile), so the size depends on batch and max_query_len then.
+ * 128-row query tile), so the size depends on batch and max_query_len then; the
+ * general kernel's key-split partials (at most 2 x CUs x 16 x (head_dim + 2) x 4
+ * bytes) fit inside the same size.
  */
 int ss_paged_attention_workspace_size(int64_t batch, int n_q, int n_kv, int head_dim,
                                       int max_query_len, int dtype, int64_t* bytes);

@@ -16,6 +16,9 @@ int64_t prefill_row_cap(int n_rep, int max_query_len);
 int launch_prefill(const AttnParams& p, int dtype, int head_dim, int max_query_len, int* work,
                    int64_t work_bytes, hipStream_t stream, bool planned);
 int read_status(int* flags, int clear, hipStream_t stream);
+int64_t general_workspace_bound(int n_q, int n_kv, int head_dim, int max_query_len);
+int launch_general(const AttnParams& p, int dtype, int head_dim, int max_query_len, bool vec, void* ws,
+                   int64_t ws_bytes, hipStream_t stream);
 }  // namespace ss
 
 namespace {
@@ -24,22 +27,25 @@ using ss::AttnParams;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Shapes every entry point accepts: GQA, bf16 / fp16 / fp32, head_dim 1..256, any
+// block size up to 1024 (the reference's Triton decode: head_dim <= 256, block_size
+// <= 128, any float dtype; triton_paged.py:22-23,283-284).
 int check_common(const char* who, int n_q, int n_kv, int head_dim, int block_size, int dtype,
                  int max_blocks, int64_t num_blocks) {
   if (n_kv < 1 || n_q < 1 || n_q % n_kv != 0) {
     ss_host::set_error("%s: GQA requires n_q %% n_kv == 0, got n_q=%d n_kv=%d", who, n_q, n_kv);
     return SS_ERR_INVALID;
   }
-  if (dtype != SS_DTYPE_BF16 && dtype != SS_DTYPE_F16) {
-    ss_host::set_error("%s: dtype code %d not supported (bf16 and fp16 only)", who, dtype);
+  if (dtype != SS_DTYPE_BF16 && dtype != SS_DTYPE_F16 && dtype != SS_DTYPE_F32) {
+    ss_host::set_error("%s: dtype code %d not supported (bf16, fp16, fp32)", who, dtype);
     return SS_ERR_UNSUPPORTED;
   }
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256) {
-    ss_host::set_error("%s: head_dim %d not supported (64, 128, 256)", who, head_dim);
+  if (head_dim < 1 || head_dim > 256) {
+    ss_host::set_error("%s: head_dim %d not supported (1..256)", who, head_dim);
     return SS_ERR_UNSUPPORTED;
   }
-  if (block_size < 4 || block_size > 1024 || (block_size & (block_size - 1)) != 0) {
-    ss_host::set_error("%s: block_size %d not supported (power of two, 4..1024)", who, block_size);
+  if (block_size < 1 || block_size > 1024) {
+    ss_host::set_error("%s: block_size %d not supported (1..1024)", who, block_size);
     return SS_ERR_UNSUPPORTED;
   }
   if (max_blocks < 0 || num_blocks < 0) {
@@ -49,15 +55,38 @@ int check_common(const char* who, int n_q, int n_kv, int head_dim, int block_siz
   return SS_OK;
 }
 
-int check_strides(const char* who, const int64_t* s, int n) {
-  for (int i = 0; i < n; ++i) {
-    if (s[i] % 8 != 0) {
-      ss_host::set_error("%s: stride %lld is not a multiple of 8 elements (16-byte rows required)", who,
-                         (long long)s[i]);
-      return SS_ERR_UNSUPPORTED;
-    }
-  }
-  return SS_OK;
+// dtype and head_dim of the MFMA kernels (bf16 / fp16, head_dim 64, 128 or 256).
+bool mfma_dtype_dim(int dtype, int head_dim) {
+  return (dtype == SS_DTYPE_BF16 || dtype == SS_DTYPE_F16) && (head_dim == 64 || head_dim == 128 || head_dim == 256);
+}
+
+bool strides_mult(const int64_t* s, int n, int64_t m) {
+  for (int i = 0; i < n; ++i)
+    if (s[i] % m != 0) return false;
+  return true;
+}
+
+// Which kernels a call takes: the MFMA decode / prefill kernels when the dtype, head_dim,
+// block size (a power of two, at least 4) and every 16-byte row condition allow, else the
+// general kernel (paged_general.hip); vec: the general kernel may read the cache rows in
+// 16-byte pieces.
+struct Route {
+  bool mfma;
+  bool vec;
+};
+
+Route route(int dtype, int head_dim, int block_size, const void* q, const void* out, const void* k_cache,
+            const void* v_cache, const int64_t* q_strides, int nq, const int64_t* o_strides, int no,
+            const int64_t c_strides[3]) {
+  const int elem = dtype == SS_DTYPE_F32 ? 4 : 2;
+  const bool planes16 = aligned16(k_cache) && aligned16(v_cache) && strides_mult(c_strides, 3, 16 / elem) &&
+                        ((int64_t)head_dim * elem) % 16 == 0;
+  Route r;
+  r.mfma = mfma_dtype_dim(dtype, head_dim) && block_size >= 4 && (block_size & (block_size - 1)) == 0 &&
+           planes16 && strides_mult(q_strides, nq, 8) && strides_mult(o_strides, no, 8) && aligned16(q) &&
+           aligned16(out);
+  r.vec = planes16;
+  return r;
 }
 
 void fill_common(AttnParams& p, const void* q, void* out, const void* k_cache, const void* v_cache,
@@ -93,7 +122,9 @@ int64_t decode_part_bytes(int dtype, int head_dim, int n_q, int n_kv, int max_qu
 }
 
 int run(AttnParams& p, int dtype, int head_dim, int max_query_len, void* workspace, int64_t ws_bytes,
-        hipStream_t stream, bool decode_rows, bool prefill_rows) {
+        hipStream_t stream, bool decode_rows, bool prefill_rows, const Route& rt) {
+  // shapes outside the MFMA tiles: one general launch covers every row of the call
+  if (!rt.mfma) return ss::launch_general(p, dtype, head_dim, max_query_len, rt.vec, workspace, ws_bytes, stream);
   p.rmax = ss::decode_rows_for(max_query_len, p.n_rep);
   p.row_cap = prefill_rows ? (int)std::min<int64_t>(ss::prefill_row_cap(p.n_rep, max_query_len), 0x7fffffff) : 0;
   const int64_t dec_bytes = decode_part_bytes(dtype, head_dim, p.n_q, p.n_kv, max_query_len);
@@ -135,7 +166,12 @@ extern "C" int ss_paged_attention_workspace_size(int64_t batch, int n_q, int n_k
     return SS_ERR_INVALID;
   }
   const int mq = max_query_len < 1 ? 1 : max_query_len;
-  *bytes = decode_part_bytes(dtype, head_dim, n_q, n_kv, mq) + ss::prefill_work_bytes(batch, n_q / n_kv, mq);
+  // the block size and strides are not known here: cover the general kernel too
+  const int64_t gen = ss::general_workspace_bound(n_q, n_kv, head_dim, mq);
+  const int64_t mfma = mfma_dtype_dim(dtype, head_dim)
+                           ? decode_part_bytes(dtype, head_dim, n_q, n_kv, mq) + ss::prefill_work_bytes(batch, n_q / n_kv, mq)
+                           : 0;
+  *bytes = mfma > gen ? mfma : gen;
   return SS_OK;
 }
 
@@ -158,17 +194,11 @@ extern "C" int ss_paged_attention(const void* q, void* out, const void* k_cache,
     ss_host::set_error("%s: batch %lld too large", who, (long long)batch);
     return SS_ERR_UNSUPPORTED;
   }
-  if ((st = check_strides(who, q_strides, 3)) != SS_OK) return st;
-  if ((st = check_strides(who, o_strides, 3)) != SS_OK) return st;
-  if ((st = check_strides(who, c_strides, 3)) != SS_OK) return st;
-  if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache)) {
-    ss_host::set_error("%s: q, out and cache planes must be 16-byte aligned", who);
-    return SS_ERR_UNSUPPORTED;
-  }
-  if (!block_tables || !seq_lens) {
-    ss_host::set_error("%s: null block_tables or seq_lens", who);
+  if (!q || !out || !k_cache || !v_cache || !block_tables || !seq_lens) {
+    ss_host::set_error("%s: null q, out, cache plane, block_tables or seq_lens", who);
     return SS_ERR_INVALID;
   }
+  const Route rt = route(dtype, head_dim, block_size, q, out, k_cache, v_cache, q_strides, 3, o_strides, 3, c_strides);
   AttnParams p = {};
   fill_common(p, q, out, k_cache, v_cache, block_tables, seq_lens, batch, n_q, n_kv, max_blocks,
               block_size, num_blocks, c_strides, bt_stride, scale);
@@ -181,7 +211,7 @@ extern "C" int ss_paged_attention(const void* q, void* out, const void* k_cache,
   p.o_st = o_strides[1];
   p.o_sh = o_strides[2];
   const bool decode = (int64_t)tq * p.n_rep <= ss::kDecodeRows;
-  return run(p, dtype, head_dim, tq, workspace, workspace_bytes, (hipStream_t)stream, decode, !decode);
+  return run(p, dtype, head_dim, tq, workspace, workspace_bytes, (hipStream_t)stream, decode, !decode, rt);
 }
 
 namespace {
@@ -206,17 +236,11 @@ int varlen_impl(const char* who, const void* q, void* out, const void* k_cache, 
                        (long long)total_tokens);
     return SS_ERR_UNSUPPORTED;
   }
-  if ((st = check_strides(who, q_strides, 2)) != SS_OK) return st;
-  if ((st = check_strides(who, o_strides, 2)) != SS_OK) return st;
-  if ((st = check_strides(who, c_strides, 3)) != SS_OK) return st;
-  if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache)) {
-    ss_host::set_error("%s: q, out and cache planes must be 16-byte aligned", who);
-    return SS_ERR_UNSUPPORTED;
-  }
-  if (!block_tables || !cu_seqlens || !context_lens) {
-    ss_host::set_error("%s: null block_tables, cu_seqlens or context_lens", who);
+  if (!q || !out || !k_cache || !v_cache || !block_tables || !cu_seqlens || !context_lens) {
+    ss_host::set_error("%s: null q, out, cache plane, block_tables, cu_seqlens or context_lens", who);
     return SS_ERR_INVALID;
   }
+  const Route rt = route(dtype, head_dim, block_size, q, out, k_cache, v_cache, q_strides, 2, o_strides, 2, c_strides);
   AttnParams p = {};
   fill_common(p, q, out, k_cache, v_cache, block_tables, context_lens, batch, n_q, n_kv, max_blocks,
               block_size, num_blocks, c_strides, bt_stride, scale);
@@ -231,7 +255,7 @@ int varlen_impl(const char* who, const void* q, void* out, const void* k_cache, 
   p.o_sh = o_strides[1];
   const bool prefill = (int64_t)max_query_len * p.n_rep > ss::kDecodeRows;
   return run(p, dtype, head_dim, max_query_len, workspace, workspace_bytes, (hipStream_t)stream, true,
-             prefill);
+             prefill, rt);
 }
 
 // Scratch of the no-alloc entry point: one array per GPU, held until the process
@@ -342,6 +366,10 @@ PrefixPlan prefix_plan(int64_t batch, int n_q, int n_kv, int head_dim, int block
                        int dtype) {
   PrefixPlan pl;
   const int n_rep = n_q / n_kv;
+  if (!mfma_dtype_dim(dtype, head_dim)) {  // the general kernel, one query token per sequence
+    pl.dec = ss::general_workspace_bound(n_q, n_kv, head_dim, 1);
+    return pl;
+  }
   pl.dec = decode_part_bytes(dtype, head_dim, n_q, n_kv, 1);
   // the prefill's tiled kernel (head_dim <= 128, blocks of 16+ tokens) carries the
   // prefix pass and the decode kernel the suffixes (n_rep <= 16); other shapes, and
@@ -415,17 +443,11 @@ extern "C" int ss_paged_attention_shared_prefix(const void* q, void* out, const 
     ss_host::set_error("%s: batch %lld too large", who, (long long)batch);
     return SS_ERR_UNSUPPORTED;
   }
-  if ((st = check_strides(who, q_strides, 2)) != SS_OK) return st;
-  if ((st = check_strides(who, o_strides, 2)) != SS_OK) return st;
-  if ((st = check_strides(who, c_strides, 3)) != SS_OK) return st;
-  if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache)) {
-    ss_host::set_error("%s: q, out and cache planes must be 16-byte aligned", who);
-    return SS_ERR_UNSUPPORTED;
-  }
-  if (!block_tables || !seq_lens) {
-    ss_host::set_error("%s: null block_tables or seq_lens", who);
+  if (!q || !out || !k_cache || !v_cache || !block_tables || !seq_lens) {
+    ss_host::set_error("%s: null q, out, cache plane, block_tables or seq_lens", who);
     return SS_ERR_INVALID;
   }
+  const Route rt = route(dtype, head_dim, block_size, q, out, k_cache, v_cache, q_strides, 2, o_strides, 2, c_strides);
   const PrefixPlan pl = prefix_plan(batch, n_q, n_kv, head_dim, block_size, prefix_blocks, dtype);
   if (!workspace || workspace_bytes < pl.total()) {
     ss_host::set_error("%s: workspace of %lld bytes, needs %lld", who, (long long)workspace_bytes,
@@ -445,9 +467,9 @@ extern "C" int ss_paged_attention_shared_prefix(const void* q, void* out, const 
   p.o_sb = o_strides[0];
   p.o_sh = o_strides[1];
   p.o_st = 0;
-  if (!pl.cascade) {
+  if (!pl.cascade || !rt.mfma) {
     const bool dec = p.n_rep <= ss::kDecodeRows;
-    return run(p, dtype, head_dim, 1, ws, pl.dec + pl.work, s, dec, !dec);
+    return run(p, dtype, head_dim, 1, ws, pl.dec + pl.work, s, dec, !dec, rt);
   }
 
   float* lse = (float*)(ws + pl.dec + pl.work);

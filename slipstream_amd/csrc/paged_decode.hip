@@ -990,14 +990,20 @@ static int launch_decode_typed(AttnParams p, int max_query_len, char* ws, int64_
 // so a bit that a kernel on another stream ORs in meanwhile is never erased unseen (it
 // is either in this read or still in the word for the next one); such a kernel's bits
 // show up only once it has run.
+// The general kernels (paged_general.hip) keep a word of their own; both are taken.
+int general_status_take(int clear, hipStream_t stream);
+int general_status_value(int* v);
+
 int read_status(int* flags, int clear, hipStream_t stream) {
   hipLaunchKernelGGL(status_take_kernel, dim3(1), dim3(1), 0, stream, clear);
   if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
+  if (general_status_take(clear, stream) != SS_OK) return SS_ERR_LAUNCH;
   if (hipStreamSynchronize(stream) != hipSuccess) return SS_ERR_LAUNCH;
-  int v = 0;
+  int v = 0, vg = 0;
   if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_status_seen), sizeof(int), 0, hipMemcpyDeviceToHost) != hipSuccess)
     return SS_ERR_LAUNCH;
-  *flags = v;
+  if (general_status_value(&vg) != SS_OK) return SS_ERR_LAUNCH;
+  *flags = v | vg;
   return SS_OK;
 }
 

@@ -13,6 +13,12 @@ entries are masked, a query row with no visible key returns zeros.
 stream described by ``cu_seqlens`` / ``context_lens`` (decode and prefill rows
 mixed), equal to the per-sequence calls concatenated.
 
+Shapes: bf16, fp16 and fp32 caches, any head_dim up to 256 and any block size up to
+1024 -- the range the reference's Triton decode serves (``triton_paged.py:22-23,283-284``).
+bf16/fp16 with head_dim 64, 128 or 256 and power-of-two blocks of at least 4 tokens
+take the MFMA kernels; every other shape takes the general kernel
+(``csrc/paged_general.hip``).
+
 There is no CPU path and no fallback: non-device tensors raise, and an
 unsupported shape raises ``RuntimeError`` from the HIP library.
 """
@@ -26,7 +32,7 @@ import torch
 from slipstream_amd import _ffi
 from slipstream_amd.kernels._common import cache_planes, require_device, unit_last_stride
 
-_SUPPORTED = (torch.bfloat16, torch.float16)
+_SUPPORTED = (torch.bfloat16, torch.float16, torch.float32)
 _WS_BYTES: dict[tuple, int] = {}
 
 
@@ -73,6 +79,14 @@ def _workspace(device: torch.device, batch: int, n_q: int, n_kv: int, head_dim: 
     return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
+def _planes(kv_cache: torch.Tensor, layer_idx: int, who: str) -> tuple[int, int, tuple[int, int, int]]:
+    """K/V plane addresses and strides; the kernels index head_dim with unit stride
+    (16-byte alignment only decides between the MFMA and the general kernels)."""
+    if kv_cache.stride(5) != 1:
+        raise _ffi.KernelError(f"{who}: kv_cache must have unit head_dim stride")
+    return cache_planes(kv_cache, layer_idx, who, aligned=False)
+
+
 def _int32(x: torch.Tensor) -> torch.Tensor:
     return (x if x.dtype == torch.int32 else x.to(torch.int32)).contiguous()
 
@@ -104,12 +118,12 @@ def paged_attention(
     require_device("paged_attention", q, kv_cache, block_tables, seq_lens)
     if q.dtype not in _SUPPORTED or kv_cache.dtype != q.dtype:
         raise _ffi.KernelError(
-            f"unsupported dtypes q={q.dtype} kv_cache={kv_cache.dtype} (bf16/fp16, equal)"
+            f"unsupported dtypes q={q.dtype} kv_cache={kv_cache.dtype} (bf16/fp16/fp32, equal)"
         )
     q = unit_last_stride(q)
     block_tables = _int32(block_tables)
     seq_lens = _int32(seq_lens.reshape(-1))
-    k_ptr, v_ptr, c_str = cache_planes(kv_cache, layer_idx, "paged_attention")
+    k_ptr, v_ptr, c_str = _planes(kv_cache, layer_idx, "paged_attention")
     out = torch.empty((batch, tq, n_q, head_dim), device=q.device, dtype=q.dtype)
     code = _ffi.dtype_code(q.dtype)
     ws = _workspace(q.device, batch, n_q, n_kv, head_dim, tq, code)
@@ -199,7 +213,7 @@ def paged_attention_shared_prefix(
     require_device("paged_attention_shared_prefix", q, kv_cache, block_tables, seq_lens)
     if q.dtype not in _SUPPORTED or kv_cache.dtype != q.dtype:
         raise _ffi.KernelError(
-            f"unsupported dtypes q={q.dtype} kv_cache={kv_cache.dtype} (bf16/fp16, equal)"
+            f"unsupported dtypes q={q.dtype} kv_cache={kv_cache.dtype} (bf16/fp16/fp32, equal)"
         )
     q = unit_last_stride(q)
     block_tables = _int32(block_tables)
@@ -209,7 +223,7 @@ def paged_attention_shared_prefix(
             raise ValueError("block_tables rows differ inside the shared prefix")
         if int(seq_lens.min()) < prefix_blocks * block_size:
             raise ValueError("a sequence is shorter than the shared prefix")
-    k_ptr, v_ptr, c_str = cache_planes(kv_cache, layer_idx, "paged_attention_shared_prefix")
+    k_ptr, v_ptr, c_str = _planes(kv_cache, layer_idx, "paged_attention_shared_prefix")
     out = torch.empty((batch, 1, n_q, head_dim), device=q.device, dtype=q.dtype)
     code = _ffi.dtype_code(q.dtype)
     key = (q.device.index, batch, n_q, n_kv, head_dim, block_size, prefix_blocks, code)
@@ -359,7 +373,7 @@ def paged_attention_varlen(
     require_device("paged_attention_varlen", q, kv_cache, block_tables, cu_seqlens, context_lens)
     if q.dtype not in _SUPPORTED or kv_cache.dtype != q.dtype:
         raise _ffi.KernelError(
-            f"unsupported dtypes q={q.dtype} kv_cache={kv_cache.dtype} (bf16/fp16, equal)"
+            f"unsupported dtypes q={q.dtype} kv_cache={kv_cache.dtype} (bf16/fp16/fp32, equal)"
         )
     q = unit_last_stride(q)
     block_tables = _int32(block_tables)
@@ -367,7 +381,7 @@ def paged_attention_varlen(
     ctx = _int32(context_lens.reshape(-1))
     if _debug():
         _check_stream(cu, total, max_query_len)
-    k_ptr, v_ptr, c_str = cache_planes(kv_cache, layer_idx, "paged_attention_varlen")
+    k_ptr, v_ptr, c_str = _planes(kv_cache, layer_idx, "paged_attention_varlen")
     code = _ffi.dtype_code(q.dtype)
     ws = _workspace(q.device, batch, n_q, n_kv, head_dim, max(1, max_query_len), code)
     status = _ffi.lib().ss_paged_attention_varlen(

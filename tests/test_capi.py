@@ -56,9 +56,21 @@ def test_argument_errors_need_no_device():
                                 z, z, z, 0, 1.0, _ffi.SS_DTYPE_BF16, None, 0, None)
     assert st == _ffi.SS_ERR_INVALID
     assert b"GQA" in lib.ss_last_error()
-    st = lib.ss_paged_attention(None, None, None, None, None, None, 1, 8, 8, 96, 1, 1, 16, 1,
+    # head_dim above 256 (the reference's Triton bound, triton_paged.py:22) and unknown
+    # dtypes are unsupported; every head_dim up to 256 and fp32 are served
+    st = lib.ss_paged_attention(None, None, None, None, None, None, 1, 8, 8, 320, 1, 1, 16, 1,
                                 z, z, z, 0, 1.0, _ffi.SS_DTYPE_BF16, None, 0, None)
     assert st == _ffi.SS_ERR_UNSUPPORTED
+    st = lib.ss_paged_attention(None, None, None, None, None, None, 1, 8, 8, 96, 1, 1, 16, 1,
+                                z, z, z, 0, 1.0, 9, None, 0, None)
+    assert st == _ffi.SS_ERR_UNSUPPORTED
+    st = lib.ss_paged_attention(None, None, None, None, None, None, 1, 8, 8, 96, 1, 1, 12, 1,
+                                z, z, z, 0, 1.0, _ffi.SS_DTYPE_F32, None, 0, None)
+    assert st == _ffi.SS_ERR_INVALID and b"null" in lib.ss_last_error()
+    for dt in (_ffi.SS_DTYPE_F32, _ffi.SS_DTYPE_BF16):
+        out = ctypes.c_int64(-1)
+        assert lib.ss_paged_attention_workspace_size(4, 8, 2, 80, 1, dt, ctypes.byref(out)) == _ffi.SS_OK
+        assert out.value > 0
     with pytest.raises(ValueError):
         _ffi.check(_ffi.SS_ERR_INVALID, "probe")
     with pytest.raises(RuntimeError):
