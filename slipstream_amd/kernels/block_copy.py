@@ -53,12 +53,63 @@ def ordered_batches(pairs: list[tuple[int, int]]) -> list[list[tuple[int, int]]]
     return batches
 
 
-def _check_ids(pairs: list[tuple[int, int]], n_src: int, n_dst: int) -> None:
-    for s, d in pairs:
-        if not 0 <= s < n_src:
-            raise ValueError(f"source block {s} outside [0, {n_src})")
-        if not 0 <= d < n_dst:
-            raise ValueError(f"destination block {d} outside [0, {n_dst})")
+def _check_ids(pairs: np.ndarray, n_src: int, n_dst: int) -> None:
+    """``pairs`` is an int64 ``[n, 2]`` array of (src, dst) rows."""
+    src, dst = pairs[:, 0], pairs[:, 1]
+    bad = (src < 0) | (src >= n_src)
+    if bad.any():
+        raise ValueError(f"source block {int(src[bad.argmax()])} outside [0, {n_src})")
+    bad = (dst < 0) | (dst >= n_dst)
+    if bad.any():
+        raise ValueError(f"destination block {int(dst[bad.argmax()])} outside [0, {n_dst})")
+
+
+def _independent(pairs: np.ndarray, n_blocks: int) -> bool:
+    """True when the pairs may all run at once (the criterion of ``ordered_batches``):
+    distinct destinations, none of them another pair's source (the block manager's
+    copy-on-write targets are fresh free blocks). The sources are distinct (dict keys);
+    ids lie in ``[0, n_blocks)``."""
+    src, dst = pairs[:, 0], pairs[:, 1]
+    if np.bincount(dst, minlength=n_blocks).max(initial=0) > 1:
+        return False
+    is_src = np.zeros(n_blocks, dtype=bool)
+    is_src[src] = True
+    return not (is_src[dst] & (src != dst)).any()
+
+
+class _Uploader:
+    """Per-device pinned staging and device buffers for the pair lists of dict calls,
+    grown as needed and reused: a call waits for the previous call's copy out of the
+    staging buffer (an event) before it overwrites it, so no pinned allocation and no
+    full synchronisation happen per call."""
+
+    def __init__(self) -> None:
+        self.host: dict[int, torch.Tensor] = {}
+        self.dev: dict[int, torch.Tensor] = {}
+        self.done: dict[int, torch.cuda.Event] = {}
+
+    def upload(self, pairs: np.ndarray, device: torch.device) -> torch.Tensor:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        n = pairs.shape[0]
+        host, dev = self.host.get(idx), self.dev.get(idx)
+        if host is None or host.shape[0] < n:
+            cap = max(n, 1024)
+            if idx in self.done:
+                self.done[idx].synchronize()
+            host = self.host[idx] = torch.empty((cap, 2), dtype=torch.int64, pin_memory=True)
+            dev = self.dev[idx] = torch.empty((cap, 2), dtype=torch.int64, device=device)
+        elif idx in self.done:
+            self.done[idx].synchronize()  # the previous copy has left the staging buffer
+        host[:n].numpy()[...] = pairs
+        dev[:n].copy_(host[:n], non_blocking=True)
+        ev = self.done.get(idx)
+        if ev is None:
+            ev = self.done[idx] = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(device))
+        return dev[:n]
+
+
+_UPLOADER = _Uploader()
 
 
 def _launch(dst: torch.Tensor, src: torch.Tensor, mapping, device: torch.device) -> None:
@@ -85,11 +136,18 @@ def _launch(dst: torch.Tensor, src: torch.Tensor, mapping, device: torch.device)
         if mapping.shape[0]:
             run(mapping.contiguous(), mapping.shape[0])
         return
-    pairs = list(mapping.items())
+    n = len(mapping)
+    pairs = np.empty((n, 2), dtype=np.int64)
+    pairs[:, 0] = np.fromiter(mapping.keys(), dtype=np.int64, count=n)
+    pairs[:, 1] = np.fromiter(mapping.values(), dtype=np.int64, count=n)
     _check_ids(pairs, snb, dnb)
-    for batch in ordered_batches(pairs):
-        host = torch.from_numpy(np.asarray(batch, dtype=np.int64).reshape(-1, 2)).pin_memory()
-        run(host.to(device, non_blocking=True), len(batch))
+    # the common case (fresh destinations) is one launch; pairs that depend on each other
+    # run in dict order, batch by batch (only a copy inside one cache can depend)
+    indep = src is not dst or _independent(pairs, dnb)
+    batches = [pairs] if indep else [np.asarray(b, dtype=np.int64).reshape(-1, 2)
+                                     for b in ordered_batches([tuple(r) for r in pairs.tolist()])]
+    for batch in batches:
+        run(_UPLOADER.upload(batch, device), batch.shape[0])
 
 
 def copy_blocks(kv_cache: torch.Tensor, src_to_dst) -> None:

@@ -280,12 +280,3 @@ def w4a16_linear(k: int, n: int, m: int, device="cuda", seed: int = 0, group_siz
     x = torch.randn((m, k), generator=gen, device=device, dtype=torch.float32).to(act)
     return W4A16Linear(x=x, qweight=qweight, scales=scales, qzeros=qzeros, group_size=group_size)
 
-
-def w4a16_reference_fp32(lin: W4A16Linear) -> torch.Tensor:
-    """fp32 dequant-then-matmul on the operands' device: ``x.float() @ ((q - z) * s).T``."""
-    n, k, g = lin.n, lin.k, lin.group_size
-    shifts = torch.arange(0, 32, 4, device=lin.qweight.device, dtype=torch.int64)
-    words = lin.qweight.to(torch.int64) & 0xFFFFFFFF
-    q = ((words.unsqueeze(-1) >> shifts) & 0xF).view(n, k // g, g).float()
-    w = (q - lin.qzeros.float().unsqueeze(-1)) * lin.scales.float().unsqueeze(-1)
-    return lin.x.float() @ w.view(n, k).t()

@@ -338,6 +338,24 @@ def test_ordered_batches_reproduce_sequential_copies():
         assert sum(len(b) for b in ordered_batches(pairs)) == len(pairs)
 
 
+def test_independent_pairs_run_in_one_batch():
+    """The dict path's vectorised test: a list with distinct destinations that are never
+    sources is exactly a list ordered_batches keeps whole, so one launch gives the
+    one-by-one result; every other list goes through ordered_batches."""
+    from slipstream_amd.kernels.block_copy import _check_ids, _independent, ordered_batches
+
+    rng = np.random.default_rng(6)
+    for _ in range(300):
+        d = {int(s): int(v) for s, v in rng.integers(0, 8, (int(rng.integers(1, 10)), 2))}  # dict: distinct sources
+        pairs = np.array(list(d.items()), dtype=np.int64).reshape(-1, 2)
+        whole = len(ordered_batches(list(d.items()))) == 1
+        assert _independent(pairs, 8) == whole, pairs
+    with pytest.raises(ValueError, match="source block 9"):
+        _check_ids(np.array([[1, 2], [9, 3]]), 8, 8)
+    with pytest.raises(ValueError, match="destination block -1"):
+        _check_ids(np.array([[1, -1]]), 8, 8)
+
+
 # ---------------------------------------------------------------- rotary embedding
 
 
