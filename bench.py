@@ -47,6 +47,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the host-side reference timing")
     ap.add_argument("--skip-extra", action="store_true", help="headline only (no packed / prefix lines)")
+    ap.add_argument("--case", default=None,
+                    help="with --only w4a16: name, name:m or :m (qkv / o / gate / down / gate_up); with --only "
+                         "prefix: plain or cascade -- one workload's dispatches per run (a profiling aid)")
     ap.add_argument("--only", choices=["all", "decode", "c1", "packed", "prefix", "w4a16", "block_copy", "rope_cache",
                                        "norm_act", "copy"], default="all",
                     help="decode (C2 step) / c1 / packed (C3) / prefix (C4) / w4a16 (C5) / block_copy / rope_cache / "
@@ -316,7 +319,16 @@ C5_SHAPES = [(4096, 6144, "qkv"), (4096, 4096, "o"), (4096, 14336, "gate"), (409
 ROTATE_BYTES = 640 << 20  # distinct weight bytes cycled per case: > 2x the 256 MB MALL
 
 
-def w4a16_section(dev, steps: int, warmup: int, cpu: bool = False) -> dict:
+def _case_filter(case: str | None):
+    """``--case`` of the profiling aids: "name", "name:m" or ":m" selects W4A16 cases
+    (name qkv / o / gate / down / gate_up), "plain" or "cascade" the C4 leg."""
+    if not case or ":" not in case and case in ("plain", "cascade"):
+        return lambda name, m: True
+    want_name, _, want_m = case.partition(":")
+    return lambda name, m: (not want_name or want_name == name) and (not want_m or int(want_m) == m)
+
+
+def w4a16_section(dev, steps: int, warmup: int, cpu: bool = False, case: str | None = None) -> dict:
     """C5: W4A16 linears of one Llama-3-8B layer at M in {1, 16, 64, 256}.
 
     Each case cycles through enough weight copies that the MALL cannot serve
@@ -336,8 +348,11 @@ def w4a16_section(dev, steps: int, warmup: int, cpu: bool = False) -> dict:
     fused_us = {}  # the quantized MLP's layout: gate and up as one 4096 x 28672 linear
     cpu_layer_us = {}
     th = _cpu_setup() if cpu else None
+    keep = _case_filter(case)
     for k, n, name in C5_SHAPES + [(4096, 2 * 14336, "gate_up")]:
         if name == "up":  # same shape as gate: timed once, counted twice in the layer total
+            continue
+        if not any(keep(name, m) for m in (1, 16, 64, 256)):
             continue
         base = workloads.w4a16_linear(k, n, 256, device=dev, seed=k + n)
         copies = max(2, min(64, -(-ROTATE_BYTES // base.weight_bytes())))
@@ -348,6 +363,8 @@ def w4a16_section(dev, steps: int, warmup: int, cpu: bool = False) -> dict:
         if cpu and name != "gate_up":
             host = (base.x.cpu(), base.qweight.cpu(), base.scales.cpu(), base.qzeros.cpu())
         for m in (1, 16, 64, 256):
+            if not keep(name, m):
+                continue
             x = base.x[:m].contiguous()
             idx = [0]
 
@@ -677,7 +694,8 @@ def packed_section(args, dev, cpu: bool) -> dict:
 
 
 def prefix_section(args, dev, cpu: bool) -> dict:
-    """C4: decode over prefix-cache tables (128 sequences sharing a 2048-token prefix)."""
+    """C4: decode over prefix-cache tables (128 sequences sharing a 2048-token prefix).
+    ``--case plain`` / ``cascade`` times one leg alone (a profiling aid)."""
     from slipstream_amd import workloads
     from slipstream_amd.kernels import paged_attention_decode, paged_attention_shared_prefix
 
@@ -691,6 +709,11 @@ def prefix_section(args, dev, cpu: bool) -> dict:
         return paged_attention_shared_prefix(pq, p.kv_cache, p.block_tables, p.context_lens, 0, p.scale, 16,
                                              p.shared_blocks)
 
+    if args.case in ("plain", "cascade"):
+        fn = pref if args.case == "plain" else casc
+        ms, _, _ = time_runs(fn, args.steps, args.warmup)
+        ms_g = graph_time(fn, 8, max(3, args.steps // 8))
+        return {"leg": args.case, "us_per_launch": round(ms * 1e3, 2), "us_per_launch_graph": round(ms_g * 1e3, 2)}
     ms_pref, _, _ = time_runs(pref, args.steps, args.warmup)
     ms_casc, _, _ = time_runs(casc, args.steps, args.warmup)
     ms_pref_g = graph_time(pref, 8, max(3, args.steps // 8))
@@ -753,7 +776,7 @@ def main() -> int:
         "c1": lambda: c1_section(args, dev, False),
         "packed": lambda: packed_section(args, dev, False),
         "prefix": lambda: prefix_section(args, dev, False),
-        "w4a16": lambda: w4a16_section(dev, args.steps, args.warmup),
+        "w4a16": lambda: w4a16_section(dev, args.steps, args.warmup, case=args.case),
         "block_copy": lambda: block_copy_section(dev, args.steps, args.warmup),
         "norm_act": lambda: norm_act_section(dev, args.steps, args.warmup),
         "rope_cache": lambda: rope_cache_section(dev, args.steps, args.warmup),
