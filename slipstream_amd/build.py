@@ -12,6 +12,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -53,8 +54,33 @@ def _compile(src: Path, obj: Path) -> None:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
 
 
+HOST_EXT = "_host_pairs"
+
+
+def host_ext_path() -> Path:
+    """The CPython extension of host helpers (``csrc/host_pairs.c``), built beside the library."""
+    return OUT_DIR / (HOST_EXT + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
+
+
+def _build_host_ext() -> Path:
+    """``csrc/host_pairs.c`` -> the extension module (gcc, CPython headers; host code only)."""
+    src = CSRC / "host_pairs.c"
+    target = host_ext_path()
+    tmp = target.with_name(target.name + ".tmp")
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        raise RuntimeError("gcc not found: needed for the host helper extension")
+    cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", f"-I{sysconfig.get_paths()['include']}", str(src), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"gcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, target)
+    return target
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile every HIP source and link the shared library; returns its path."""
+    """Compile every HIP source and link the shared library, then the host helper
+    extension; returns the library's path."""
     OUT_DIR.mkdir(parents=True, exist_ok=True)
     obj_dir = OUT_DIR / "obj"
     obj_dir.mkdir(exist_ok=True)
@@ -72,8 +98,10 @@ def build(verbose: bool = False) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, target)
+    ext = _build_host_ext()
     if verbose:
         print(f"built {target}")
+        print(f"built {ext}")
     return target
 
 

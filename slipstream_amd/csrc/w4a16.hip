@@ -512,15 +512,16 @@ __global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
 //   - The loop is VALU-bound rather than MFMA- or memory-bound: per stage and wave
 //     (MT = NS = 4, the m > 64 tiles when this was measured) 64 MFMAs against about
 //     300 VALU instructions -- the nibble
-//     unpack (8 per 32-bit word), the fold (2 FMAs per accumulator element) and the
+//     unpack (7 per 32-bit word), the fold (one FMA per accumulator element) and the
 //     activation staging (its row sums as v_dot2 against ones: 48 fewer per stage
 //     than converting and adding each value, 124.6 -> 118.5 us for the C5 layer at
 //     m = 64, no change at m = 256). With loads and stores taken out it still took 48 us of the
 //     4096 x 28672, m = 256 linear's 101 us; prefetching activations PF stages ahead
 //     as well changed nothing.
 //   - Per 32-key step the MFMA accumulates G = sum x (MAGIC + q) for every
-//     (activation tile, weight tile) pair; one fold per stage:
-//       acc += s * G - s * (MAGIC + z) * X.
+//     (activation tile, weight tile) pair; one fold per stage, acc += s * G, and at the
+//     end of the range the zero-point term of all its stages at once,
+//       acc -= sum over stages of X * s * (MAGIC + z)   (a rank-1 product per stage).
 // Every range is a whole number of PF stages (host-checked).
 constexpr int kOutOfRange = 0x40000000;  // buffer offset past any operand (< 2^31 bytes)
 
@@ -579,11 +580,18 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
   const int total = TR * gr;
   uint32_t sbits[TB];
   int zv[TB];
+  // entry q = (row q / gr, group q % gr). The quotient through a float reciprocal (a
+  // 32-bit integer division is some twenty instructions): the table holds at most
+  // kTileTableMax / 8 = 5120 entries of at least 64 rows, so q < 5120 and gr <= 80;
+  // (q + 0.5) / gr sits at least 0.5 / gr >= 0.006 from an integer, and the two
+  // roundings move it by at most q * 2^-23 < 0.001
+  const float inv_gr = 1.0f / (float)gr;
+  auto table_row = [&](int q) { return (int)(((float)q + 0.5f) * inv_gr); };
   auto table_load = [&](int q0) {
 #pragma unroll
     for (int u = 0; u < TB; ++u) {
       const int q = min(q0 + NTHR * u, total - 1);
-      const int r = q / gr, gl = q - r * gr;
+      const int r = table_row(q), gl = q - r * gr;
       const int si = min(nb + r, p.n - 1) * p.groups + g0 + gl;
       sbits[u] = scale_bits(rsc, si, esize);
       zv[u] = __builtin_amdgcn_raw_buffer_load_b32(rzp, si * 4, 0, 0);
@@ -594,7 +602,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
     for (int u = 0; u < TB; ++u) {
       const int q = q0 + NTHR * u;
       if (q < total) {
-        const int r = q / gr, gl = q - r * gr;
+        const int r = table_row(q), gl = q - r * gr;
         const float sc = decode_scale_masked(sbits[u], f16_mask, bf16_mask);
         s_sz[r * srow + gl] = float2{sc, sc * (E::kMagic + (float)zv[u])};
       }
@@ -655,7 +663,8 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
       store16(&s_x[buf][r][8 * c], permute_x(src[u]));
       // every lane of the row stores the same total: no branch, so the loop body stays
       // one block (a block boundary lets the compiler sink the folds to the loop end,
-      // keeping every stage's partial sums live)
+      // keeping every stage's partial sums live); sixteen lanes storing one word cost no
+      // bank-conflict cycles (SQ_LDS_BANK_CONFLICT reads 0 for such stores)
       xrow[r] = sum;
     }
   };
@@ -1685,6 +1694,10 @@ template <typename T, int MT, int NS, int PF, int WV>
 int launch_w4a16_tile(const W4Params& p, const W4Plan& pl, float* part, hipStream_t stream) {
   if (16 * NS * WV != 64 * pl.ns) {
     ss_host::set_error("w4a16 gemm: tiled plan of %d rows per workgroup, kernel of %d", 64 * pl.ns, 16 * NS * WV);
+    return SS_ERR_UNSUPPORTED;
+  }
+  if (pl.kchunk % PF != 0) {  // the loop runs whole rounds of PF stages
+    ss_host::set_error("w4a16 gemm: K range of %d stages for a %d-stage prefetch ring", pl.kchunk, PF);
     return SS_ERR_UNSUPPORTED;
   }
   static bool attr_set = false;  // per instantiation; the attribute is process-wide

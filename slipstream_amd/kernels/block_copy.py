@@ -53,28 +53,30 @@ def ordered_batches(pairs: list[tuple[int, int]]) -> list[list[tuple[int, int]]]
     return batches
 
 
-def _check_ids(pairs: np.ndarray, n_src: int, n_dst: int) -> None:
-    """``pairs`` is an int64 ``[n, 2]`` array of (src, dst) rows."""
-    src, dst = pairs[:, 0], pairs[:, 1]
-    bad = (src < 0) | (src >= n_src)
-    if bad.any():
-        raise ValueError(f"source block {int(src[bad.argmax()])} outside [0, {n_src})")
-    bad = (dst < 0) | (dst >= n_dst)
-    if bad.any():
-        raise ValueError(f"destination block {int(dst[bad.argmax()])} outside [0, {n_dst})")
+_HOST_PAIRS = None
 
 
-def _independent(pairs: np.ndarray, n_blocks: int) -> bool:
-    """True when the pairs may all run at once (the criterion of ``ordered_batches``):
-    distinct destinations, none of them another pair's source (the block manager's
-    copy-on-write targets are fresh free blocks). The sources are distinct (dict keys);
-    ids lie in ``[0, n_blocks)``."""
-    src, dst = pairs[:, 0], pairs[:, 1]
-    if np.bincount(dst, minlength=n_blocks).max(initial=0) > 1:
-        return False
-    is_src = np.zeros(n_blocks, dtype=bool)
-    is_src[src] = True
-    return not (is_src[dst] & (src != dst)).any()
+def _host_pairs():
+    """The host helper extension (``csrc/host_pairs.c``): ``pack(mapping, addr, cap, n_src,
+    n_dst, check) -> (n, independent)`` writes a dict's (src, dst) pairs as int64 rows into
+    a buffer, raising ValueError for an id outside its cache, and with ``check`` reports
+    whether the pairs may all run at once -- the criterion of ``ordered_batches``: distinct
+    destinations, none of them another pair's source (the block manager's copy-on-write
+    targets are fresh free blocks)."""
+    global _HOST_PAIRS
+    if _HOST_PAIRS is None:
+        import importlib.util
+
+        from slipstream_amd import build
+
+        path = build.host_ext_path()
+        if not path.exists():
+            raise _ffi.KernelError(f"{path.name} is not built: run `python -m slipstream_amd.build`")
+        spec = importlib.util.spec_from_file_location("slipstream_amd._host_pairs", path)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        _HOST_PAIRS = mod
+    return _HOST_PAIRS
 
 
 class _Uploader:
@@ -88,25 +90,37 @@ class _Uploader:
         self.dev: dict[int, torch.Tensor] = {}
         self.done: dict[int, torch.cuda.Event] = {}
 
-    def upload(self, pairs: np.ndarray, device: torch.device) -> torch.Tensor:
-        idx = device.index if device.index is not None else torch.cuda.current_device()
-        n = pairs.shape[0]
-        host, dev = self.host.get(idx), self.dev.get(idx)
+    @staticmethod
+    def _index(device: torch.device) -> int:
+        return device.index if device.index is not None else torch.cuda.current_device()
+
+    def staging(self, n: int, device: torch.device) -> torch.Tensor:
+        """The pinned int64 ``[cap, 2]`` staging buffer (cap >= n), free to overwrite."""
+        idx = self._index(device)
+        host = self.host.get(idx)
+        if idx in self.done:
+            self.done[idx].synchronize()  # the previous copy has left the staging buffer
         if host is None or host.shape[0] < n:
             cap = max(n, 1024)
-            if idx in self.done:
-                self.done[idx].synchronize()
             host = self.host[idx] = torch.empty((cap, 2), dtype=torch.int64, pin_memory=True)
-            dev = self.dev[idx] = torch.empty((cap, 2), dtype=torch.int64, device=device)
-        elif idx in self.done:
-            self.done[idx].synchronize()  # the previous copy has left the staging buffer
-        host[:n].numpy()[...] = pairs
+            self.dev[idx] = torch.empty((cap, 2), dtype=torch.int64, device=device)
+        return host
+
+    def send(self, n: int, device: torch.device) -> torch.Tensor:
+        """Copy the staging buffer's first n rows to the device buffer (stream-ordered)."""
+        idx = self._index(device)
+        host, dev = self.host[idx], self.dev[idx]
         dev[:n].copy_(host[:n], non_blocking=True)
         ev = self.done.get(idx)
         if ev is None:
             ev = self.done[idx] = torch.cuda.Event()
         ev.record(torch.cuda.current_stream(device))
         return dev[:n]
+
+    def upload(self, pairs: np.ndarray, device: torch.device) -> torch.Tensor:
+        n = pairs.shape[0]
+        self.staging(n, device)[:n].numpy()[...] = pairs
+        return self.send(n, device)
 
 
 _UPLOADER = _Uploader()
@@ -136,17 +150,19 @@ def _launch(dst: torch.Tensor, src: torch.Tensor, mapping, device: torch.device)
         if mapping.shape[0]:
             run(mapping.contiguous(), mapping.shape[0])
         return
-    n = len(mapping)
-    pairs = np.empty((n, 2), dtype=np.int64)
-    pairs[:, 0] = np.fromiter(mapping.keys(), dtype=np.int64, count=n)
-    pairs[:, 1] = np.fromiter(mapping.values(), dtype=np.int64, count=n)
-    _check_ids(pairs, snb, dnb)
-    # the common case (fresh destinations) is one launch; pairs that depend on each other
-    # run in dict order, batch by batch (only a copy inside one cache can depend)
-    indep = src is not dst or _independent(pairs, dnb)
-    batches = [pairs] if indep else [np.asarray(b, dtype=np.int64).reshape(-1, 2)
-                                     for b in ordered_batches([tuple(r) for r in pairs.tolist()])]
-    for batch in batches:
+    if not isinstance(mapping, dict):
+        mapping = dict(mapping)
+    # the pairs go straight into the pinned staging buffer, checked on the way; the common
+    # case (fresh destinations) is one launch; pairs that depend on each other run in dict
+    # order, batch by batch (only a copy inside one cache can depend)
+    host = _UPLOADER.staging(len(mapping), device)
+    n, indep = _host_pairs().pack(mapping, host.data_ptr(), host.shape[0], snb, dnb, src is dst)
+    if indep:
+        run(_UPLOADER.send(n, device), n)
+        return
+    pairs = host[:n].numpy().copy()
+    for b in ordered_batches([tuple(r) for r in pairs.tolist()]):
+        batch = np.asarray(b, dtype=np.int64).reshape(-1, 2)
         run(_UPLOADER.upload(batch, device), batch.shape[0])
 
 

@@ -339,21 +339,36 @@ def test_ordered_batches_reproduce_sequential_copies():
 
 
 def test_independent_pairs_run_in_one_batch():
-    """The dict path's vectorised test: a list with distinct destinations that are never
-    sources is exactly a list ordered_batches keeps whole, so one launch gives the
-    one-by-one result; every other list goes through ordered_batches."""
-    from slipstream_amd.kernels.block_copy import _check_ids, _independent, ordered_batches
+    """The dict path's packer (csrc/host_pairs.c): the pairs it writes are the dict's items
+    in order, and it calls a mapping independent exactly when ordered_batches keeps the
+    whole list as one batch (so one launch gives the one-by-one result; every other list
+    goes through ordered_batches). Ids outside a cache raise the wrapper's ValueError."""
+    from slipstream_amd.kernels.block_copy import _host_pairs, ordered_batches
 
+    pack = _host_pairs().pack
+    buf = np.zeros((16, 2), dtype=np.int64)
+    addr = buf.ctypes.data
     rng = np.random.default_rng(6)
-    for _ in range(300):
-        d = {int(s): int(v) for s, v in rng.integers(0, 8, (int(rng.integers(1, 10)), 2))}  # dict: distinct sources
-        pairs = np.array(list(d.items()), dtype=np.int64).reshape(-1, 2)
-        whole = len(ordered_batches(list(d.items()))) == 1
-        assert _independent(pairs, 8) == whole, pairs
+    for trial in range(600):
+        nb = int(rng.integers(2, 12))
+        d = {int(s): int(v) for s, v in rng.integers(0, nb, (int(rng.integers(1, 12)), 2))}  # distinct sources
+        n, indep = pack(d, addr, buf.shape[0], nb, nb, True)
+        assert n == len(d) and buf[:n].tolist() == [list(kv) for kv in d.items()], d
+        assert bool(indep) == (len(ordered_batches(list(d.items()))) == 1), d
+        assert pack(d, addr, buf.shape[0], nb, nb, False)[1] == 1  # no check: one launch (two caches)
+    # numpy integers are ids too; an empty mapping packs nothing
+    assert pack({np.int64(3): np.int32(4)}, addr, 16, 8, 8, True) == (1, 1) and buf[0].tolist() == [3, 4]
+    assert pack({}, addr, 16, 8, 8, True) == (0, 1)
     with pytest.raises(ValueError, match="source block 9"):
-        _check_ids(np.array([[1, 2], [9, 3]]), 8, 8)
+        pack({1: 2, 9: 3}, addr, 16, 8, 8, True)
     with pytest.raises(ValueError, match="destination block -1"):
-        _check_ids(np.array([[1, -1]]), 8, 8)
+        pack({1: -1}, addr, 16, 8, 8, True)
+    with pytest.raises(ValueError, match="destination block 8"):
+        pack({1: 8}, addr, 16, 16, 8, False)  # destination cache of 8 blocks
+    with pytest.raises(ValueError, match="pairs for a buffer"):
+        pack({i: i + 20 for i in range(17)}, addr, 16, 64, 64, True)
+    with pytest.raises(TypeError):
+        pack({1.5: 2}, addr, 16, 8, 8, True)
 
 
 # ---------------------------------------------------------------- rotary embedding
