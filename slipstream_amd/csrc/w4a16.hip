@@ -512,16 +512,15 @@ __global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
 //   - The loop is VALU-bound rather than MFMA- or memory-bound: per stage and wave
 //     (MT = NS = 4, the m > 64 tiles when this was measured) 64 MFMAs against about
 //     300 VALU instructions -- the nibble
-//     unpack (7 per 32-bit word), the fold (one FMA per accumulator element) and the
+//     unpack (7 per 32-bit word), the fold (2 FMAs per accumulator element) and the
 //     activation staging (its row sums as v_dot2 against ones: 48 fewer per stage
 //     than converting and adding each value, 124.6 -> 118.5 us for the C5 layer at
 //     m = 64, no change at m = 256). With loads and stores taken out it still took 48 us of the
 //     4096 x 28672, m = 256 linear's 101 us; prefetching activations PF stages ahead
 //     as well changed nothing.
 //   - Per 32-key step the MFMA accumulates G = sum x (MAGIC + q) for every
-//     (activation tile, weight tile) pair; one fold per stage, acc += s * G, and at the
-//     end of the range the zero-point term of all its stages at once,
-//       acc -= sum over stages of X * s * (MAGIC + z)   (a rank-1 product per stage).
+//     (activation tile, weight tile) pair; one fold per stage:
+//       acc += s * G - s * (MAGIC + z) * X.
 // Every range is a whole number of PF stages (host-checked).
 constexpr int kOutOfRange = 0x40000000;  // buffer offset past any operand (< 2^31 bytes)
 
@@ -537,11 +536,9 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
   constexpr int BM = 16 * MT;
   constexpr int LROW = 128 + 8;  // LDS row of an activation stage, elements (16-byte skew)
   __shared__ __attribute__((aligned(16))) T s_x[2][BM][LROW];
+  __shared__ __attribute__((aligned(16))) float s_sum[2][BM];
   extern __shared__ __attribute__((aligned(16))) char s_dyn[];
-  // [kchunk + 1][BM] row sums X of the range's activation stages (the last row takes
-  // stages past the range), then the scale table [TR rows][gr + 1] (s, s*(MAGIC+z))
-  float* const s_xall = (float*)s_dyn;
-  float2* const s_sz = (float2*)(s_dyn + (size_t)(kchunk + 1) * BM * sizeof(float));
+  float2* const s_sz = (float2*)s_dyn;  // [TR rows][gr + 1] (s, s*(MAGIC+z))
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -649,9 +646,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
   // the chunk's sum as four v_dot2 against a pair of ones (fp32 accumulation): a quarter
   // of the instructions of converting and adding the eight values one by one
   const uint32_t one2 = in_vgpr(E::kOnePair);
-  // st: the stage's index in the range (kchunk and above: past the range)
-  auto stage_x = [&](int buf, const u32x4 (&src)[XC], int st) {
-    float* const xrow = s_xall + (size_t)min(st, kchunk) * BM;
+  auto stage_x = [&](int buf, const u32x4 (&src)[XC]) {
 #pragma unroll
     for (int u = 0; u < XC; ++u) {
       const int q = threadIdx.x + NTHR * u;
@@ -663,9 +658,8 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
       store16(&s_x[buf][r][8 * c], permute_x(src[u]));
       // every lane of the row stores the same total: no branch, so the loop body stays
       // one block (a block boundary lets the compiler sink the folds to the loop end,
-      // keeping every stage's partial sums live); sixteen lanes storing one word cost no
-      // bank-conflict cycles (SQ_LDS_BANK_CONFLICT reads 0 for such stores)
-      xrow[r] = sum;
+      // keeping every stage's partial sums live)
+      s_sum[buf][r] = sum;
     }
   };
 
@@ -690,16 +684,17 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
         for (int mt = 0; mt < MT; ++mt) G[mt][ns] = Elem<T>::mfma(a[mt], b, s == 0 ? zero4 : G[mt][ns]);
       }
     }
-    // acc += s G; the zero-point term -s (MAGIC + z) X is applied for the whole range at
-    // the end (a rank-1 product per stage, on the fp32 MFMA)
+    f32x4 X[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) X[mt] = *reinterpret_cast<const f32x4*>(&s_sum[buf][mt * 16 + 4 * kg]);
     const int gl = ((i << 7) / p.g) - g0;
 #pragma unroll
     for (int ns = 0; ns < NS; ++ns) {
-      const float sc = s_sz[t_row[ns] + gl].x;
+      const float2 sz = s_sz[t_row[ns] + gl];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[mt][ns][e] = fmaf(sc, G[mt][ns][e], acc[mt][ns][e]);
+        for (int e = 0; e < 4; ++e) acc[mt][ns][e] = fmaf(sz.x, G[mt][ns][e], fmaf(-sz.y, X[mt][e], acc[mt][ns][e]));
     }
   };
 
@@ -715,7 +710,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
     table_load(q0);
     table_store(q0);
   }
-  stage_x(0, xr[0], 0);
+  stage_x(0, xr[0]);
   __syncthreads();  // the scale table and the first activation stage
   for (int i = i0; i < i1; i += PF) {
 #pragma unroll
@@ -727,30 +722,8 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
       __builtin_amdgcn_sched_barrier(0);
       load_w(i + u + PF, ring[u]);
       __builtin_amdgcn_sched_barrier(0);
-      stage_x(buf ^ 1, xr[(u + 1) & 1], i + u + 1 - i0);
+      stage_x(buf ^ 1, xr[(u + 1) & 1]);
       __syncthreads();
-    }
-  }
-  // The zero-point term of the range: acc[m][n] -= sum over its stages j of X_j[m]
-  // s_j (MAGIC + z_j)[n], four stages per fp32 MFMA 16x16x4 (A = -X: lane (row ln, stage
-  // kg); B = s (MAGIC + z): lane (stage kg, weight row ln); the result has the
-  // accumulators' layout). The loop's last barrier has made every stage's X visible.
-  {
-    const int nst = i1 - i0;
-    for (int j0 = 0; j0 < nst; j0 += 4) {
-      const int j = j0 + kg;
-      const bool jv = j < nst;
-      const int jc = jv ? j : nst - 1;
-      const int gl = (((i0 + jc) << 7) / p.g) - g0;
-      float bz[NS];
-#pragma unroll
-      for (int ns = 0; ns < NS; ++ns) bz[ns] = jv ? s_sz[t_row[ns] + gl].y : 0.f;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const float xa = jv ? -s_xall[(size_t)jc * BM + mt * 16 + ln] : 0.f;
-#pragma unroll
-        for (int ns = 0; ns < NS; ++ns) acc[mt][ns] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, bz[ns], acc[mt][ns], 0, 0, 0);
-      }
     }
   }
 
@@ -1476,12 +1449,6 @@ size_t tile_table_bytes(int ns, int kchunk, int g) {
   return (size_t)64 * ns * (gr + 1) * 8;
 }
 
-// Dynamic LDS of the tiled kernel: the range's activation row sums ((kchunk + 1) x BM
-// floats), then the scale table.
-size_t tile_dyn_bytes(int ns, int mt, int kchunk, int g) {
-  return (size_t)(kchunk + 1) * 16 * mt * 4 + tile_table_bytes(ns, kchunk, g);
-}
-
 bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
   if (!pl.wide || m < 2) return false;
   // m <= 16 is weight-bandwidth bound and the untiled kernel shares activations
@@ -1520,11 +1487,11 @@ bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
   if (ks > 65535) return false;
   // more ranges while a range's scale table is too large; the ranges stay balanced
   int64_t per = (rounds + ks - 1) / ks;
-  while (per > 1 && tile_dyn_bytes(ns, mt, (int)(per * pf), g) > (size_t)kTileTableMax) {
+  while (per > 1 && tile_table_bytes(ns, (int)(per * pf), g) > (size_t)kTileTableMax) {
     ++ks;
     per = (rounds + ks - 1) / ks;
   }
-  if (tile_dyn_bytes(ns, mt, (int)(per * pf), g) > (size_t)kTileTableMax) return false;
+  if (tile_table_bytes(ns, (int)(per * pf), g) > (size_t)kTileTableMax) return false;
   pl.tile = true;
   pl.mt = mt, pl.ns = ns, pl.pf = pf;
   pl.n_tiles = (int)n_tiles;
@@ -1532,7 +1499,7 @@ bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
   pl.kchunk = (int)(per * pf);
   pl.ks = (int)((rounds + per - 1) / per);
   if (pl.ks > 65535) return false;
-  pl.lds = tile_dyn_bytes(ns, mt, pl.kchunk, g);
+  pl.lds = tile_table_bytes(ns, pl.kchunk, g);
   // the partials are addressed by 32-bit offsets, with kOutOfRange past all of them
   if (pl.ks > 1 && (int64_t)pl.ks * m * n * 4 >= (int64_t)kOutOfRange) return false;
   return true;
