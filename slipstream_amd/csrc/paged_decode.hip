@@ -281,6 +281,134 @@ __device__ __forceinline__ void compute_pair(const AttnParams& p, const DecodeTi
   }
 }
 
+// ---- small decode batches (one launch, no merge)
+//
+// For a padded decode call with few (sequence, KV head) pairs and short tables, one
+// workgroup per (sequence b, KV head h): its eight waves take the same query rows (the
+// qlen * n_rep <= 16 rows of the split-K kernel's tile) and an eighth of the sequence's
+// 32-key pairs each, with the decode's pair loads and pair math; wave 0 then combines
+// the eight (max, sum, output) states through LDS by log-sum-exp weight and writes the
+// rows. Every row of the call is written here (a sequence with no key gets zeros, as
+// the merge writes them), so no merge kernel follows: for C1-sized calls the split-K
+// launch's plan scan and its merge launch are most of the time.
+template <typename T, int D>
+__global__ __launch_bounds__(512) void decode_small_kernel(const AttnParams p) {
+  typedef DecodeTile<T, D> Tile;
+  constexpr int NW = 8;
+  constexpr int NACC = RowState<T, D>::NACC;
+  __shared__ float s_ml[NW][16][2];
+  __shared__ f32x4 s_acc[NW - 1][NACC][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int b = blockIdx.x / p.n_kv, h = blockIdx.x - (blockIdx.x / p.n_kv) * p.n_kv;
+  int qlen;
+  int64_t qoff;
+  seq_queries(p, b, qlen, qoff);
+  qlen = __builtin_amdgcn_readfirstlane(qlen);
+  const int R = qlen * p.n_rep;
+  const bool row_ok = n < R;
+  const int j = row_ok ? n / p.n_rep : 0;
+  const int hq = h * p.n_rep + (row_ok ? n - j * p.n_rep : 0);
+  // wave w takes pairs w, w + NW, ...: its first pair's table entries and K/V rows are
+  // requested before the sequence's length arrives (through the whole table, every
+  // block checked), and the V rows past the length are zeroed once it has (keys past
+  // it are masked by the pair math; a zero V row keeps stale values of unused slots
+  // out of the product)
+  const int32_t* table = p.bt + (int64_t)b * p.bt_stride;
+  const int cap = p.max_blocks << p.bs_shift;
+  DecodeTile<T, D> ta, tb;
+  load_pair<T, D>(p, table, cap, wave, h, lane, ta);
+  const int ctx = __builtin_amdgcn_readfirstlane(kv_len(p, b));
+  const int kvt = seq_kv_tokens(p, ctx);
+  const int lim = row_ok ? ctx - qlen + j + 1 : 0;
+  const int lim_eff = lim < kvt ? lim : kvt;
+  int lim_min = row_ok ? lim_eff : 0x7fffffff;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) lim_min = min(lim_min, __shfl_xor(lim_min, o));
+  lim_min = __builtin_amdgcn_readfirstlane(lim_min);
+  u32x4 qop[Tile::KS];
+  {
+    const T* qrow = (const T*)p.q + (int64_t)b * p.q_sb + (qoff + j) * p.q_st + (int64_t)hq * p.q_sh;
+#pragma unroll
+    for (int s2 = 0; s2 < Tile::KS; ++s2) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      qop[s2] = row_ok ? load16(qrow + 32 * s2 + 8 * g) : z;
+    }
+  }
+  RowState<T, D> st;
+#pragma unroll
+  for (int a = 0; a < NACC; ++a) st.acc[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+  st.m = kNegBig;
+  st.l = 0.f;
+  const int npairs = (kvt + kPairTokens - 1) / kPairTokens;
+  int pi = wave;
+  if (pi < npairs) {
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool live = pi * kPairTokens + 16 * x + 4 * g + e < kvt;
+#pragma unroll
+        for (int mt = 0; mt < Tile::MT; ++mt)
+          ta.v[mt][4 * x + e] = live ? ta.v[mt][4 * x + e] : u32x4{0u, 0u, 0u, 0u};
+      }
+    while (true) {
+      load_pair<T, D>(p, table, kvt, pi + NW, h, lane, tb);
+      compute_pair<T, D>(p, ta, qop, pi, lim_eff, lim_min, lane, st);
+      pi += NW;
+      if (pi >= npairs) break;
+      load_pair<T, D>(p, table, kvt, pi + NW, h, lane, ta);
+      compute_pair<T, D>(p, tb, qop, pi, lim_eff, lim_min, lane, st);
+      pi += NW;
+      if (pi >= npairs) break;
+    }
+  }
+  const float lt = sum_across_rows(st.l);
+  if (g == 0) {
+    s_ml[wave][n][0] = st.m;
+    s_ml[wave][n][1] = lt;
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int a = 0; a < NACC; ++a) s_acc[wave - 1][a][lane] = st.acc[a];
+  }
+  __syncthreads();
+  if (wave != 0 || !row_ok) return;
+  // log-sum-exp combination of the waves' states (a wave without pairs has max
+  // kNegBig and sum 0; if no wave had a key the sum stays 0 and the row is zeros)
+  float mx = st.m;
+#pragma unroll
+  for (int w = 1; w < NW; ++w) mx = fmaxf(mx, s_ml[w][n][0]);
+  const float f0 = fast_exp2(st.m - mx);
+  float lsum = lt * f0;
+#pragma unroll
+  for (int a = 0; a < NACC; ++a) st.acc[a] *= f0;
+#pragma unroll
+  for (int w = 1; w < NW; ++w) {
+    const float f = fast_exp2(s_ml[w][n][0] - mx);
+    lsum += f * s_ml[w][n][1];
+#pragma unroll
+    for (int a = 0; a < NACC; ++a) st.acc[a] += f * s_acc[w - 1][a][lane];
+  }
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  if (p.lse && g == 0) p.lse[lse_index(p, b, qoff, j, hq)] = row_lse(mx, lsum);
+  T* orow = (T*)p.out + (int64_t)b * p.o_sb + (qoff + j) * p.o_st + (int64_t)hq * p.o_sh;
+#pragma unroll
+  for (int mt = 0; mt < Tile::MT; ++mt) {
+    const int dbase = 128 * mt + 32 * g;
+    if (dbase < D) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f32x4* a = &st.acc[mt * 8];
+        const u32x4 o = {Elem<T>::pack2(a[0][e] * inv, a[1][e] * inv), Elem<T>::pack2(a[2][e] * inv, a[3][e] * inv),
+                         Elem<T>::pack2(a[4][e] * inv, a[5][e] * inv), Elem<T>::pack2(a[6][e] * inv, a[7][e] * inv)};
+        store16(orow + dbase + 8 * e, o);
+      }
+    }
+  }
+}
+
 // ---- scalar block-table path (block_size >= 16: a 16-token tile lies in one block)
 //
 // The tile's physical block is wave-uniform, so its table entry is a scalar load
@@ -899,6 +1027,9 @@ static int heads_per_wg(int n_kv) {
 // Decode workgroups: one per CU (the stream-K ranges of all head groups together).
 static int decode_resident_wgs() { return ss_host::device_cu_count(); }
 
+// Longest table (keys) a call may have for the small-batch decode kernel.
+constexpr int64_t kSmallDecodeKeys = 1024;
+
 // Decode split-K geometry: number of workgroups and bytes of workspace.
 struct DecodeGeometry {
   int hpw, n_hgroups, n_ranges, n_wg, rmax;
@@ -946,6 +1077,18 @@ static int launch_decode_typed(AttnParams p, int max_query_len, char* ws, int64_
     ss_host::set_error("paged attention: workspace of %lld bytes, decode needs %lld", (long long)ws_bytes,
                        (long long)g.total());
     return SS_ERR_WORKSPACE;
+  }
+  // small padded decode calls: one workgroup per (sequence, KV head), no merge (see
+  // decode_small_kernel): at most two workgroups per CU and tables of at most 1024 keys
+  // (four pairs per wave)
+  if constexpr (D <= 128) {
+    if (!p.cu && p.px_n == 0 && p.row_cap == 0 && p.chunk_tokens == 0 && p.ctx_shift == 0 &&
+        (int64_t)p.tq * p.n_rep <= p.rmax && (int64_t)p.max_blocks * p.block_size <= kSmallDecodeKeys &&
+        (int64_t)p.batch * p.n_kv <= 2 * (int64_t)decode_resident_wgs()) {
+      hipLaunchKernelGGL((decode_small_kernel<T, D>), dim3((unsigned)((int64_t)p.batch * p.n_kv)), dim3(512), 0,
+                         stream, p);
+      return ss_host::launch_status("paged attention decode (small)");
+    }
   }
   // carve: [rec][ml][o]
   p.ws_rec = (int*)ws;
