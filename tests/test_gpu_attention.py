@@ -163,6 +163,41 @@ def test_decode_table_holes_and_zero_lengths(device):
     assert torch.count_nonzero(out[3]) == 0
 
 
+@pytest.mark.parametrize("lens", [[3, 17, 40, 250, 511], [3, 17, 40, 250, 2000]])
+def test_decode_ignores_stale_nan_slots(device, lens):
+    """Slots past a sequence's length (the rest of its last block, and blocks its table
+    lists past the length) hold NaN: the output must not see them. Short tables take the
+    one-launch small-batch kernel (which requests the first pair before the length is
+    known), the 2000-key table the split-K kernel."""
+    print(f"decode stale NaN lens={lens}", flush=True)
+    b = workloads.build_batch(lens, [1] * len(lens), n_q=14, n_kv=2, head_dim=64, block_size=16,
+                              dtype=torch.float16, device="cpu", seed=21)
+    width = b.block_tables.shape[1]
+    kv = b.kv_cache
+    used = set()
+    for t, n in zip(b.tables_host, lens):
+        for i, blk in enumerate(t):
+            lo = i * 16
+            if lo >= n:
+                kv[0, :, blk] = float("nan")
+            elif lo + 16 > n:
+                kv[0, :, blk, n - lo:] = float("nan")
+            used.add(blk)
+    ref = _oracle_padded(b)
+    # tables padded with real (NaN) blocks past each length, as a block manager may leave them
+    bt = b.block_tables.clone()
+    spare = [x for x in range(kv.shape[2]) if x not in used]
+    for i, t in enumerate(b.tables_host):
+        for c in range(len(t), width):
+            bt[i, c] = spare[(i * width + c) % len(spare)]
+    kv[0, :, spare] = float("nan")
+    b.block_tables = bt
+    _to(b, device)
+    out = paged_attention_decode(b.padded_q(), b.kv_cache, b.block_tables, b.context_lens, 0, b.scale, 16)
+    assert torch.isfinite(out).all()
+    assert_attn_close(out, ref, f"stale NaN lens={lens}")
+
+
 def test_decode_head_dim_64_and_256(device):
     for d in (64, 256):
         b = workloads.build_batch([5, 77, 600], [1, 1, 1], n_q=16, n_kv=4, head_dim=d, block_size=16,
