@@ -844,8 +844,8 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
   }
 }
 
-// Skinny kernel (2 <= m <= 16, g == 128): bandwidth-bound shapes without a K split
-// across workgroups. A workgroup owns 16*NS weight rows and KW waves; wave w takes the
+// Skinny kernel (2 <= m <= 16, and up to m = 64 for 4096 x 4096, g == 128): bandwidth-
+// bound shapes without a K split across workgroups. A workgroup owns 16*NS weight rows and KW waves; wave w takes the
 // 128*ST keys [w*128*ST, (w+1)*128*ST) of those rows and of the 16*MT activation rows,
 // P stages of 128 keys in flight (weights non-temporal). Per stage and weight tile: four
 // MFMAs G = sum x (MAGIC + q), and per activation tile four MFMAs X = sum x against an
@@ -1512,7 +1512,13 @@ bool plan_tile(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
 constexpr size_t kSkinnyLdsMax = 128 * 1024;
 
 bool plan_skinny(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
-  if (!pl.wide || m < 2 || m > 16 || g != 128) return false;
+  if (!pl.wide || m < 2 || m > 64 || g != 128) return false;
+  // 16 < m <= 64 only for the 4096 x 4096 class (one 16-row activation tile per
+  // workgroup row, the weights re-read per tile from the L2 / MALL): o at m = 17 / 32 / 48
+  // / 64 7.6 / 7.8 / 11.5 / 11.6 us against 9.9 / 11.2 / 12.0 / 12.7 on the tiled
+  // kernel; wider or deeper linears lose (gate at m = 64 43.6 against 20.0, down 59.2
+  // against 24.3)
+  if (m > 16 && (n > 4096 || k > 4096)) return false;
   // the widest linears take the tiled kernel (the stacked gate/up projection, 4096 x
   // 28672, 224 weight tiles, unsplit: 22.2 against 24.0 us at m = 16, 22.0 against 22.7
   // at m = 8; for narrower N the skinny kernel stays well ahead)
