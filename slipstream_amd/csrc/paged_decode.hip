@@ -99,11 +99,31 @@ struct DecodeTile {
   int valid;        // bit x: tile x of this lane row's V tokens lives in a valid block
 };
 
-// Issue the loads of pair `pi` of the sequence whose table is `table`.
-// Every load is unconditional: absent keys read the zero row instead.
+// The block-table entries a lane needs for pair `pi`: the block of its K token (tile x)
+// and of its V tokens (tile x).
+struct PairPhys {
+  int k[2];
+  int v[2];
+};
+
+__device__ __forceinline__ PairPhys fetch_pair_phys(const AttnParams& p, const int32_t* table, int pi, int lane) {
+  const int n = lane & 15, g = lane >> 4;
+  PairPhys ph;
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    int bk = (pi * kPairTokens + 16 * x + n) >> p.bs_shift;
+    int bv = (pi * kPairTokens + 16 * x + 4 * g) >> p.bs_shift;
+    ph.k[x] = table[bk < p.max_blocks ? bk : p.max_blocks - 1];
+    ph.v[x] = table[bv < p.max_blocks ? bv : p.max_blocks - 1];
+  }
+  return ph;
+}
+
+// Issue the K/V loads of pair `pi` given its table entries. Every load is
+// unconditional: absent keys read the zero row instead.
 template <typename T, int D>
-__device__ __forceinline__ void load_pair(const AttnParams& p, const int32_t* table, int kvt, int pi,
-                                          int h, int lane, DecodeTile<T, D>& t) {
+__device__ __forceinline__ void load_pair_phys(const AttnParams& p, const PairPhys& ph, int kvt, int pi, int h,
+                                               int lane, DecodeTile<T, D>& t) {
   typedef DecodeTile<T, D> Tile;
   const char* kc = (const char*)p.kc;
   const char* vc = (const char*)p.vc;
@@ -115,9 +135,7 @@ __device__ __forceinline__ void load_pair(const AttnParams& p, const int32_t* ta
   for (int x = 0; x < 2; ++x) {
     // K: this lane's token is n of tile x
     const int tk = pi * kPairTokens + 16 * x + n;
-    int bi = tk >> p.bs_shift;
-    bi = bi < p.max_blocks ? bi : p.max_blocks - 1;
-    const int phys = table[bi];
+    const int phys = ph.k[x];
     const bool ok = tk < kvt && phys >= 0 && phys < p.num_blocks;
     const char* krow =
         ok ? kc + ((int64_t)phys * p.c_sb + (int64_t)(tk & bmask) * p.c_so + hoff) * (int64_t)sizeof(T)
@@ -130,9 +148,7 @@ __device__ __forceinline__ void load_pair(const AttnParams& p, const int32_t* ta
   for (int x = 0; x < 2; ++x) {
     // V: tokens 4g..4g+3 of tile x share one block (block_size >= 4)
     const int t0 = pi * kPairTokens + 16 * x + 4 * g;
-    int bi = t0 >> p.bs_shift;
-    bi = bi < p.max_blocks ? bi : p.max_blocks - 1;
-    const int phys = table[bi];
+    const int phys = ph.v[x];
     const bool okb = phys >= 0 && phys < p.num_blocks;
     if (okb) t.valid |= 1 << x;
     const int64_t base = ((int64_t)phys * p.c_sb + hoff) * (int64_t)sizeof(T);
@@ -149,6 +165,13 @@ __device__ __forceinline__ void load_pair(const AttnParams& p, const int32_t* ta
       }
     }
   }
+}
+
+// Issue the loads of pair `pi` of the sequence whose table is `table`.
+template <typename T, int D>
+__device__ __forceinline__ void load_pair(const AttnParams& p, const int32_t* table, int kvt, int pi,
+                                          int h, int lane, DecodeTile<T, D>& t) {
+  load_pair_phys<T, D>(p, fetch_pair_phys(p, table, pi, lane), kvt, pi, h, lane, t);
 }
 
 template <typename T, int D>
@@ -318,7 +341,14 @@ __global__ __launch_bounds__(512) void decode_small_kernel(const AttnParams p) {
   const int32_t* table = p.bt + (int64_t)b * p.bt_stride;
   const int cap = p.max_blocks << p.bs_shift;
   DecodeTile<T, D> ta, tb;
-  load_pair<T, D>(p, table, cap, wave, h, lane, ta);
+  {
+    // the table entries of both first pairs before any K/V load: a table load issued
+    // behind K/V loads waits for them (the vector-memory counter retires in order)
+    const PairPhys pa = fetch_pair_phys(p, table, wave, lane);
+    const PairPhys pb = fetch_pair_phys(p, table, wave + NW, lane);
+    load_pair_phys<T, D>(p, pa, cap, wave, h, lane, ta);
+    load_pair_phys<T, D>(p, pb, cap, wave + NW, h, lane, tb);
+  }
   const int ctx = __builtin_amdgcn_readfirstlane(kv_len(p, b));
   const int kvt = seq_kv_tokens(p, ctx);
   const int lim = row_ok ? ctx - qlen + j + 1 : 0;
@@ -344,24 +374,31 @@ __global__ __launch_bounds__(512) void decode_small_kernel(const AttnParams p) {
   const int npairs = (kvt + kPairTokens - 1) / kPairTokens;
   int pi = wave;
   if (pi < npairs) {
+    // the first two pairs were loaded through the whole table: zero their V rows past
+    // the length
+    auto zero_v_past = [&](DecodeTile<T, D>& t, int pt) {
 #pragma unroll
-    for (int x = 0; x < 2; ++x)
+      for (int x = 0; x < 2; ++x)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bool live = pi * kPairTokens + 16 * x + 4 * g + e < kvt;
+        for (int e = 0; e < 4; ++e) {
+          const bool live = pt * kPairTokens + 16 * x + 4 * g + e < kvt;
 #pragma unroll
-        for (int mt = 0; mt < Tile::MT; ++mt)
-          ta.v[mt][4 * x + e] = live ? ta.v[mt][4 * x + e] : u32x4{0u, 0u, 0u, 0u};
-      }
-    while (true) {
-      load_pair<T, D>(p, table, kvt, pi + NW, h, lane, tb);
-      compute_pair<T, D>(p, ta, qop, pi, lim_eff, lim_min, lane, st);
-      pi += NW;
-      if (pi >= npairs) break;
+          for (int mt = 0; mt < Tile::MT; ++mt)
+            t.v[mt][4 * x + e] = live ? t.v[mt][4 * x + e] : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    zero_v_past(ta, pi);
+    zero_v_past(tb, pi + NW);
+    compute_pair<T, D>(p, ta, qop, pi, lim_eff, lim_min, lane, st);
+    pi += NW;
+    while (pi < npairs) {  // tb holds pair pi
       load_pair<T, D>(p, table, kvt, pi + NW, h, lane, ta);
       compute_pair<T, D>(p, tb, qop, pi, lim_eff, lim_min, lane, st);
       pi += NW;
       if (pi >= npairs) break;
+      load_pair<T, D>(p, table, kvt, pi + NW, h, lane, tb);
+      compute_pair<T, D>(p, ta, qop, pi, lim_eff, lim_min, lane, st);
+      pi += NW;
     }
   }
   const float lt = sum_across_rows(st.l);
