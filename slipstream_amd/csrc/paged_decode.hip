@@ -421,12 +421,31 @@ __global__ __launch_bounds__(512) void decode_small_kernel(const AttnParams p) {
   float lsum = lt * f0;
 #pragma unroll
   for (int a = 0; a < NACC; ++a) st.acc[a] *= f0;
+  // One wave's state ahead of the adds: left to itself the compiler sank the adds to
+  // the output stores, kept all seven states of 32 floats live beside the lane's own and
+  // spilled. The empty asm makes each wave's sums exist before the wave after next is
+  // read; the next wave's state is requested before them, so its LDS latency overlaps.
+  f32x4 cur[NACC];
+#pragma unroll
+  for (int a = 0; a < NACC; ++a) cur[a] = s_acc[0][a][lane];
 #pragma unroll
   for (int w = 1; w < NW; ++w) {
+    f32x4 nxt[NACC];
+    if (w + 1 < NW) {
+#pragma unroll
+      for (int a = 0; a < NACC; ++a) nxt[a] = s_acc[w][a][lane];
+    }
     const float f = fast_exp2(s_ml[w][n][0] - mx);
     lsum += f * s_ml[w][n][1];
 #pragma unroll
-    for (int a = 0; a < NACC; ++a) st.acc[a] += f * s_acc[w - 1][a][lane];
+    for (int a = 0; a < NACC; ++a) {
+      st.acc[a] += f * cur[a];
+      asm volatile("" : "+v"(st.acc[a]));
+    }
+    if (w + 1 < NW) {
+#pragma unroll
+      for (int a = 0; a < NACC; ++a) cur[a] = nxt[a];
+    }
   }
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   if (p.lse && g == 0) p.lse[lse_index(p, b, qoff, j, hq)] = row_lse(mx, lsum);
