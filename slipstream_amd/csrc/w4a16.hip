@@ -209,8 +209,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 // reduction buffer (kw - 1) x MT*NS x 64 x f32x4.
 template <typename T, int MT, int NS, int BIT, bool WIDE, bool XLDS>
 __global__ __launch_bounds__(64 * kMaxKW) void w4a16_kernel(const W4Params p) {
-  constexpr int SPI = WIDE ? 1 : 4;      // quantisation groups (folds) per 128-key iteration
-  constexpr int UNIT = WIDE ? 128 : 32;  // keys per fold
+  constexpr int UNIT = WIDE ? 128 : 32;  // keys per fold (one quantisation group; 4 per 128-key iteration if !WIDE)
   typedef W4Elem<T> E;
   extern __shared__ __attribute__((aligned(16))) char s_dyn[];
 
