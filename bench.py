@@ -347,6 +347,7 @@ def w4a16_section(dev, steps: int, warmup: int, cpu: bool = False, case: str | N
     layer_us = {}
     fused_us = {}  # the quantized MLP's layout: gate and up as one 4096 x 28672 linear
     cpu_layer_us = {}
+    dense_layer_us = {}  # the same layer with dense bf16 weights through torch (hipBLASLt)
     th = _cpu_setup() if cpu else None
     keep = _case_filter(case)
     for k, n, name in C5_SHAPES + [(4096, 2 * 14336, "gate_up")]:
@@ -396,14 +397,38 @@ def w4a16_section(dev, steps: int, warmup: int, cpu: bool = False, case: str | N
                 layer_us[m] = layer_us.get(m, 0.0) + ms * 1e3 * (2 if name == "gate" else 1)
             if name != "gate":
                 fused_us[m] = fused_us.get(m, 0.0) + ms * 1e3
+        xs = base.x
         del qws, scs, qzs, base, host
+        torch.cuda.empty_cache()
+        # Reference point, not a baseline of this path: the same product with dense bf16
+        # weights through torch (hipBLASLt), weights rotated past the MALL the same way
+        dcopies = max(2, min(16, -(-ROTATE_BYTES // (n * k * 2))))
+        dws = [torch.randn(n, k, device=dev, dtype=torch.bfloat16) for _ in range(dcopies)]
+        for c in cases:
+            if c["linear"] != name or "dense_bf16_us" in c:
+                continue
+            xd = xs[: c["m"]].contiguous()
+            didx = [0]
+
+            def dense_call():
+                i = didx[0] % dcopies
+                didx[0] += 1
+                return torch.nn.functional.linear(xd, dws[i])
+
+            c["dense_bf16_us"] = round(graph_time(dense_call, dcopies, max(3, steps // dcopies)) * 1e3, 2)
+            if name != "gate_up":
+                dense_layer_us[c["m"]] = dense_layer_us.get(c["m"], 0.0) + c["dense_bf16_us"] * (2 if name == "gate" else 1)
+        del dws, xs
         torch.cuda.empty_cache()
     out = {"workload": "C5 W4A16 linears of one Llama-3-8B layer (qkv 4096x6144, o 4096x4096, gate/up "
                        "4096x14336, down 14336x4096), g=128, fp16 scales, zeros 8, bf16 x",
            "cases": cases, "layer_us_by_m": {str(m): round(v, 2) for m, v in layer_us.items()},
            "layer_fused_gate_up_us_by_m": {str(m): round(v, 2) for m, v in fused_us.items()},
+           "dense_bf16_layer_us_by_m": {str(m): round(v, 2) for m, v in dense_layer_us.items()},
            "note": "layer = qkv + o + gate + up + down (the reference's linears); layer_fused_gate_up = "
-                   "qkv + o + gate_up + down (W4A16MLP's layout: gate and up stacked in one launch)"}
+                   "qkv + o + gate_up + down (W4A16MLP's layout: gate and up stacked in one launch); "
+                   "dense_bf16_*: the same products with dense bf16 weights through torch.nn.functional.linear "
+                   "(hipBLASLt), a reference point for the MFMA-bound cases, not part of this path"}
     if cpu:
         out["cpu_baseline"] = _cpu_record(0.0, 3, th, "reference CPU path (unpack, fp32 dequant, cast, dense "
                                                        "matmul) per linear and M; cases[].cpu_us")
