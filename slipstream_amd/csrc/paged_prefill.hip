@@ -427,9 +427,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   }
   const float cscale = __builtin_fabsf(p.scale_log2);
-  // the query operands are in registers before the first DMA is issued, so no
-  // wait for them lands inside the pipelined loop
-  wait_vm<0>();
+  // The query operands must be in registers before the first DMA is issued, so that
+  // no wait for them lands inside the pipelined loop: the table scan below waits for
+  // its own loads, which were issued after these, before its barrier (one round trip
+  // for both; a separate wait here cost one more per item).
   // smallest causal limit over the wave's rows (rows past R do not count)
   const int wrow = min(row0 + wave * 16 * NT, R - 1);
   const int wave_lim = p.noncausal ? kvt : min(kvt, ctx - qlen + wrow / p.n_rep + 1);
