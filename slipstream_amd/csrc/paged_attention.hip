@@ -10,6 +10,11 @@ namespace ss {
 int64_t decode_workspace_bytes(int dtype, int head_dim, int n_q, int n_kv, int max_query_len);
 int launch_decode(const AttnParams& p, int dtype, int head_dim, int max_query_len, char* ws,
                   int64_t ws_bytes, hipStream_t stream);
+// shared-prefix cascade: prefix pass (pp, n_pf workgroups) and suffix decode (ps) in one
+// launch, then the merge
+int launch_cascade(const AttnParams& pp, const AttnParams& ps, int n_pf, int dtype, int head_dim, char* ws,
+                   int64_t ws_bytes, hipStream_t stream);
+int decode_heads_per_wg(int n_kv);
 int64_t prefill_work_bytes(int64_t batch, int n_rep, int max_query_len);
 int64_t prefill_row_cap(int n_rep, int max_query_len);
 // planned: work already holds the list (count, then (b << 16) | query tile per entry)
@@ -336,7 +341,8 @@ extern "C" int ss_paged_attention_varlen_noalloc(const void* q, void* out, const
 //
 // A decode batch whose block tables all begin with the same prefix_blocks blocks
 // (prefix-cache hits share full blocks) attends that prefix once for every
-// sequence's query rows instead of once per sequence, in two launches:
+// sequence's query rows instead of once per sequence. One launch (cascade_kernel)
+// runs parts 1 and 2 side by side on disjoint workgroups, the merge launch follows:
 //   1. the prefix is cut into S chunks of cb blocks; chunk s is a pseudo-sequence
 //      whose keys are the chunk (its table: entries s*cb .. of the first table row,
 //      which holds the shared prefix) and whose queries are the whole batch's (read
@@ -356,6 +362,7 @@ namespace {
 struct PrefixPlan {
   bool cascade = false;
   int cb = 0, S = 0;
+  int n_pf = 0, dec_ranges = 0;  // workgroups of the prefix pass; decode ranges per head group
   int64_t dec = 0, work = 0, lse = 0, part = 0, seq = 0;
   int64_t total() const { return dec + work + lse + part + seq; }
 };
@@ -380,11 +387,17 @@ PrefixPlan prefix_plan(int64_t batch, int n_q, int n_kv, int head_dim, int block
     pl.work = ss::prefill_work_bytes(batch, n_rep, 1);
     return pl;
   }
-  // about one prefill item per CU: items = S * row tiles * n_kv; chunks hold
-  // whole 64-key tiles
+  // The prefix pass and the suffix decode run in one launch on disjoint CUs: 7/16 of
+  // them take the prefix chunks (about one item each: items = S * row tiles * n_kv;
+  // chunks hold whole 64-key tiles) and the rest the decode ranges. Each half alone at
+  // C4 (256 CUs): the prefix pass on 84 / 112 / 140 / 168 workgroups 21.9 / 19.4 /
+  // 18.1 / 17.6 us, the suffix decode on 172 / 144 / 128 / 112 ranges 20.6 / 21.1 /
+  // 23.0 / 25.5 us.
   const int64_t per_chunk = ((batch * n_rep + 127) / 128) * n_kv;
   const int64_t cus = ss_host::device_cu_count();
-  int64_t target = (cus + per_chunk - 1) / per_chunk;
+  int64_t px_wgs = cus * 7 / 16;
+  if (px_wgs < 1) px_wgs = 1;
+  int64_t target = px_wgs / per_chunk;
   if (target < 1) target = 1;
   const int tile_blocks = 64 / block_size > 1 ? 64 / block_size : 1;
   int64_t cb = (prefix_blocks + target - 1) / target;
@@ -395,6 +408,11 @@ PrefixPlan prefix_plan(int64_t batch, int n_q, int n_kv, int head_dim, int block
   if (cb > prefix_blocks) cb = prefix_blocks;
   pl.cb = (int)cb;
   pl.S = (int)((prefix_blocks + cb - 1) / cb);
+  const int64_t items = pl.S * per_chunk;
+  pl.n_pf = (int)(items < px_wgs ? items : px_wgs);
+  const int64_t hgroups = n_kv / ss::decode_heads_per_wg(n_kv);
+  const int64_t rest = (cus - pl.n_pf) / hgroups;
+  pl.dec_ranges = (int)(rest > 1 ? rest : 1);
   const int64_t elem = 2;  // bf16 / fp16
   pl.work = 0;  // the prefix pass walks its (chunk, query tile) items in order
   pl.lse = round256(4 * (int64_t)pl.S * batch * n_q);
@@ -476,27 +494,29 @@ extern "C" int ss_paged_attention_shared_prefix(const void* q, void* out, const 
   void* part = ws + pl.dec + pl.work + pl.lse;
   float* seq_o = (float*)(ws + pl.dec + pl.work + pl.lse + pl.part);
   float* seq_ml = seq_o + batch * n_q * (int64_t)head_dim;
-  const int qtiles = (int)((batch * p.n_rep + 127) / 128);
-  {  // 1. prefix chunks as pseudo-sequences of the prefill, queries read in place
-    AttnParams pp = {};
-    fill_common(pp, q, part, k_cache, v_cache, block_tables, nullptr, pl.S, n_q, n_kv, pl.cb, block_size,
-                num_blocks, c_strides, pl.cb, scale);
-    pp.chunk_tokens = pl.cb * block_size;
-    pp.prefix_tokens = prefix_blocks * block_size;
-    pp.work_qtiles = qtiles;
-    pp.q_sb = 0;
-    pp.q_st = q_strides[0];
-    pp.q_sh = q_strides[1];
-    pp.o_sb = 0;
-    pp.o_st = (int64_t)n_q * head_dim;
-    pp.o_sh = head_dim;
-    pp.rmax = ss::decode_rows_for((int)batch, pp.n_rep);
-    pp.lse = lse;
-    pp.noncausal = 1;
-    pp.q_period = (int)batch;
-    st = ss::launch_prefill(pp, dtype, head_dim, (int)batch, nullptr, 0, s, true);
-    if (st != SS_OK) return st;
+  const int64_t qtiles = (batch * p.n_rep + 127) / 128;
+  if (qtiles > 0xFFFF || pl.S > 0x7FFF || pl.S * qtiles * n_kv > 0x7fffffff) {
+    ss_host::set_error("%s: too many query tiles for the prefix pass (%lld per chunk, %d chunks)", who,
+                       (long long)qtiles, pl.S);
+    return SS_ERR_UNSUPPORTED;
   }
+  // 1. prefix chunks as pseudo-sequences of the tiled prefill, queries read in place
+  AttnParams pp = {};
+  fill_common(pp, q, part, k_cache, v_cache, block_tables, nullptr, pl.S, n_q, n_kv, pl.cb, block_size, num_blocks,
+              c_strides, pl.cb, scale);
+  pp.chunk_tokens = pl.cb * block_size;
+  pp.prefix_tokens = prefix_blocks * block_size;
+  pp.work_qtiles = (int)qtiles;
+  pp.q_sb = 0;
+  pp.q_st = q_strides[0];
+  pp.q_sh = q_strides[1];
+  pp.o_sb = 0;
+  pp.o_st = (int64_t)n_q * head_dim;
+  pp.o_sh = head_dim;
+  pp.rmax = ss::decode_rows_for((int)batch, pp.n_rep);
+  pp.lse = lse;
+  pp.noncausal = 1;
+  pp.q_period = (int)batch;
   // 2. private suffixes: the table from column prefix_blocks on, lengths past the
   // prefix; the prefix parts are folded in where each row is finished
   AttnParams ps = p;
@@ -509,11 +529,8 @@ extern "C" int ss_paged_attention_shared_prefix(const void* q, void* out, const 
   ps.px_n = pl.S;
   ps.px_seq_o = seq_o;
   ps.px_seq_ml = seq_ml;
-  // suffixes are short (C4: about nine 32-key pairs each): one range per CU and head
-  // group at most (measured 47.6 us at C4 against 51.1 us for two; 192 and 128 ranges
-  // were slower)
-  ps.range_cap = ss_host::device_cu_count();
-  return ss::launch_decode(ps, dtype, head_dim, 1, ws, pl.dec, s);
+  ps.range_cap = pl.dec_ranges;
+  return ss::launch_cascade(pp, ps, pl.n_pf, dtype, head_dim, ws, pl.dec, s);
 }
 
 extern "C" int ss_attention_status(int* flags, int clear, void* stream) {

@@ -28,6 +28,7 @@
 //                   for d = 8*m + i. P^T comes straight out of the S^T
 //                   accumulator layout. No LDS is used.
 #include "attention_common.h"
+#include "prefill_tile.h"
 
 namespace ss {
 namespace {
@@ -548,8 +549,11 @@ __device__ __forceinline__ void load_pair_scalar(const AttnParams& p, const Scal
 // STAB: scalar block-table path (block_size >= 16); otherwise every lane looks up
 // its own block (block_size 4 and 8 put several blocks in one 16-token tile). AUX: the
 // page-load cache policy of the STAB path.
-template <typename T, int D, bool STAB, int AUX>
-__global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
+// The body of decode_kernel as workgroup bid (the shared-prefix cascade runs it in
+// the workgroups after its prefix pass). Waves past hpw (a cascade workgroup has
+// eight, CASCADE) take part in the plan's block reductions and then leave.
+template <typename T, int D, bool STAB, int AUX, bool CASCADE>
+__device__ __forceinline__ void decode_body(const AttnParams& p, const unsigned bid) {
   typedef DecodeTile<T, D> Tile;
   __shared__ int s_red[16];
   __shared__ int s_b0, s_c0;
@@ -557,10 +561,10 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int hg = blockIdx.x % p.n_hgroups;
-  const int wr = blockIdx.x / p.n_hgroups;
+  const int hg = (unsigned)bid % p.n_hgroups;  // unsigned: no sign fix-ups in the division
+  const int wr = (unsigned)bid / p.n_hgroups;
   const int h = hg * p.hpw + wave;
-  int* rec = p.ws_rec + (int64_t)blockIdx.x * 8;
+  int* rec = p.ws_rec + (int64_t)bid * 8;
 
   // ---- plan: total pairs, this range, and the sequence holding its first pair
   // pair count of this thread's first sequence, kept for the scan's first pass (one
@@ -598,6 +602,7 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
     if (s_b0 >= 0) break;
   }
   int b = __builtin_amdgcn_readfirstlane(s_b0), c = __builtin_amdgcn_readfirstlane(s_c0), pos = s_w;
+  if (CASCADE && wave >= p.hpw) return;  // no barrier follows
   // lane byte offsets of the scalar-table path: constant for the whole kernel
   const int tok_bytes = (int)(p.c_so * (int64_t)sizeof(T));
   const int head_bytes = (int)(p.c_sh * (int64_t)sizeof(T));
@@ -639,7 +644,7 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
         // a sequence finished here, which the merge completes with the prefix parts
         const int slot = c > s_w ? 1 : 0;
         const int64_t pidx = complete ? lse_index(p, b, qoff, j, hq)
-                                      : (((int64_t)blockIdx.x * 2 + slot) * p.hpw + wave) * p.rmax + n;
+                                      : (((int64_t)bid * 2 + slot) * p.hpw + wave) * p.rmax + n;
         if (row_ok) {
           float* po = (complete ? p.px_seq_o : p.ws_o) + pidx * D;
 #pragma unroll
@@ -893,6 +898,27 @@ __global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
     rec[5] = rec_c0;
     rec[6] = rec_c1;
   }
+}
+
+template <typename T, int D, bool STAB, int AUX>
+__global__ __launch_bounds__(512) void decode_kernel(const AttnParams p) {
+  decode_body<T, D, STAB, AUX, false>(p, blockIdx.x);
+}
+
+// Shared-prefix cascade in one launch: workgroups [0, n_pf) run the prefix pass (the
+// tiled prefill over the prefix chunks, pp) and the others the suffix decode's ranges
+// (ps, scalar-table walker). The two halves need nothing from each other (the merge
+// launch after them folds the prefix parts in) and each CU holds one workgroup, so
+// they run side by side on disjoint CUs: the latency-bound pieces of both (item
+// prologues, the short suffix ranges) overlap instead of adding up, with no
+// cross-queue wait of a second stream.
+template <typename T, int D, int AUX>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void cascade_kernel(
+    const AttnParams pp, const AttnParams ps, const int n_pf) {
+  if ((int)blockIdx.x < n_pf)
+    prefill_tile_body<T, D>(pp, nullptr, blockIdx.x, n_pf);
+  else
+    decode_body<T, D, true, AUX, true>(ps, blockIdx.x - n_pf);
 }
 
 // Combine the partials of every sequence cut by a range boundary (blocks
@@ -1184,6 +1210,64 @@ static int launch_decode_typed(AttnParams p, int max_query_len, char* ws, int64_
   return ss_host::launch_status("paged attention decode merge");
 }
 
+// Shared-prefix cascade: the prefix pass (pp: the tiled prefill over the prefix chunks,
+// n_pf workgroups walking its work_qtiles items) and the suffix decode (ps) in one
+// launch of cascade_kernel, then the decode merge, which folds the prefix parts in.
+// Needs the scalar-table walker and the tiled prefill: block_size >= 16, head_dim <= 128.
+template <typename T, int D>
+static int launch_cascade_typed(const AttnParams& pp, AttnParams ps, int n_pf, char* ws, int64_t ws_bytes,
+                                hipStream_t stream) {
+  if constexpr (D > 128) {
+    ss_host::set_error("shared-prefix cascade: head_dim %d above 128", D);
+    return SS_ERR_UNSUPPORTED;
+  } else {
+    const DecodeGeometry g = decode_geometry<T, D>(ps.n_kv, decode_rows_for(1, ps.n_rep));
+    if (ws_bytes < g.total()) {
+      ss_host::set_error("shared-prefix cascade: workspace of %lld bytes, decode needs %lld", (long long)ws_bytes,
+                         (long long)g.total());
+      return SS_ERR_WORKSPACE;
+    }
+    if (ps.rmax != g.rmax || ps.block_size < 16 || pp.block_size < 16 || n_pf < 1 || ps.px_n < 1) {
+      ss_host::set_error("shared-prefix cascade: invalid launch (rows %d / %d, block_size %d, %d prefix workgroups)",
+                         ps.rmax, g.rmax, ps.block_size, n_pf);
+      return SS_ERR_INVALID;
+    }
+    ps.ws_rec = (int*)ws;
+    ps.ws_ml = (float*)(ws + g.rec_bytes);
+    ps.ws_o = (float*)(ws + g.rec_bytes + g.ml_bytes);
+    ps.hpw = g.hpw;
+    ps.n_hgroups = g.n_hgroups;
+    ps.n_ranges = g.n_ranges;
+    int n_wg = g.n_wg;
+    if (ps.range_cap > 0 && ps.n_ranges > ps.range_cap) {
+      ps.n_ranges = ps.range_cap;
+      n_wg = ps.n_ranges * g.n_hgroups;
+    }
+    const int lds = 6 * TileCfg<T, D>::PLANE;
+    const int64_t pool_bytes = 2 * (int64_t)ps.num_blocks * ps.c_sb * (int64_t)sizeof(T);
+    const bool nt = pool_bytes > kMallReuseBytes;
+    const void* kern = nt ? (const void*)cascade_kernel<T, D, kNonTemporal> : (const void*)cascade_kernel<T, D, kDefaultPolicy>;
+    static bool attr_set[2] = {false, false};  // per instantiation; the attribute is process-wide
+    if (!attr_set[nt]) {
+      if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess) {
+        ss_host::set_error("shared-prefix cascade: cannot reserve %d bytes of LDS", lds);
+        return SS_ERR_UNSUPPORTED;
+      }
+      attr_set[nt] = true;
+    }
+    if (nt)
+      hipLaunchKernelGGL((cascade_kernel<T, D, kNonTemporal>), dim3(n_pf + n_wg), dim3(512), lds, stream, pp, ps,
+                         n_pf);
+    else
+      hipLaunchKernelGGL((cascade_kernel<T, D, kDefaultPolicy>), dim3(n_pf + n_wg), dim3(512), lds, stream, pp, ps,
+                         n_pf);
+    int st = ss_host::launch_status("shared-prefix cascade");
+    if (st != SS_OK) return st;
+    hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(n_wg + ps.batch), dim3(512), 0, stream, ps, n_wg);
+    return ss_host::launch_status("shared-prefix cascade merge");
+  }
+}
+
 // Read (and optionally clear) this device's status word after the work queued on
 // `stream` has finished. The read and the clear are one atomic exchange on the device,
 // so a bit that a kernel on another stream ORs in meanwhile is never erased unseen (it
@@ -1204,6 +1288,20 @@ int read_status(int* flags, int clear, hipStream_t stream) {
   if (general_status_value(&vg) != SS_OK) return SS_ERR_LAUNCH;
   *flags = v | vg;
   return SS_OK;
+}
+
+int decode_heads_per_wg(int n_kv) { return heads_per_wg(n_kv); }
+
+int launch_cascade(const AttnParams& pp, const AttnParams& ps, int n_pf, int dtype, int head_dim, char* ws,
+                   int64_t ws_bytes, hipStream_t stream) {
+  if (dtype == SS_DTYPE_BF16) {
+    if (head_dim == 64) return launch_cascade_typed<bf16_t, 64>(pp, ps, n_pf, ws, ws_bytes, stream);
+    if (head_dim == 128) return launch_cascade_typed<bf16_t, 128>(pp, ps, n_pf, ws, ws_bytes, stream);
+    return launch_cascade_typed<bf16_t, 256>(pp, ps, n_pf, ws, ws_bytes, stream);
+  }
+  if (head_dim == 64) return launch_cascade_typed<f16_t, 64>(pp, ps, n_pf, ws, ws_bytes, stream);
+  if (head_dim == 128) return launch_cascade_typed<f16_t, 128>(pp, ps, n_pf, ws, ws_bytes, stream);
+  return launch_cascade_typed<f16_t, 256>(pp, ps, n_pf, ws, ws_bytes, stream);
 }
 
 int launch_decode(const AttnParams& p, int dtype, int head_dim, int max_query_len, char* ws,
