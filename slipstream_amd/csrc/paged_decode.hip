@@ -922,8 +922,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // Combine the partials of every sequence cut by a range boundary (blocks
-// [0, n_wg)), and write the rows no attention kernel of the call writes (blocks
-// [n_wg, n_wg + batch), one per sequence):
+// [0, n_wg)); in a shared-prefix call (n_fin = n_wg) finish the sequences each range
+// completed (blocks [n_wg, 2 n_wg), apart from the split ones so that neither waits
+// for the other's loads); and write the rows no attention kernel of the call writes
+// (the last batch blocks, one per sequence):
 //  - a decode sequence with no visible key: zeros (the Triton rule, l == 0);
 //  - query rows past what this call's kernels cover, which only a packed stream
 //    whose sequence is longer than max_query_len has: zeros, and the status word
@@ -933,10 +935,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // sequence raises kStatusPrefixShort (its suffix counts as empty). In a shared-prefix
 // call the merge also folds the prefix parts into the rows it writes.
 template <typename T, int D>
-__global__ __launch_bounds__(512) void decode_merge_kernel(const AttnParams p, int n_wg) {
+__global__ __launch_bounds__(512) void decode_merge_kernel(const AttnParams p, int n_wg, int n_fin) {
   const int tid = threadIdx.x;
-  if ((int)blockIdx.x >= n_wg) {
-    const int b = blockIdx.x - n_wg;
+  if ((int)blockIdx.x >= n_wg + n_fin) {
+    const int b = blockIdx.x - n_wg - n_fin;
     int qlen;
     int64_t qoff;
     seq_queries(p, b, qlen, qoff);
@@ -985,36 +987,44 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const AttnParams p, i
     }
     return;
   }
-  const int* rec = p.ws_rec + (int64_t)blockIdx.x * 8;
-  const int hg = blockIdx.x % p.n_hgroups;
   if constexpr (D <= 128) {
-    const int c0 = rec[5], c1 = rec[6];
-    if (p.px_n > 0 && c0 >= 0) {
-      // shared-prefix cascade: the sequences this range finished (one query token
-      // each), completed with the prefix parts; one thread per (sequence, query head
-      // of the head group, 8 consecutive d). [c0, c1) spans the first and last
-      // sequence the range finished; a sequence between them with no suffix pair
-      // (seq_len == prefix tokens) was skipped by the walker, left no state here, and
-      // is written by its own per-sequence block from the prefix parts alone.
-      constexpr int DV = D / 8;
-      const int hrows = p.hpw * p.n_rep;
-      for (int u = tid; u < (c1 - c0) * hrows * DV; u += blockDim.x) {
-        const int c = u % DV, t = u / DV;
-        const int bb = c0 + t / hrows, hq = hg * hrows + t % hrows;
-        if (decode_pairs(p, bb) == 0) continue;
-        const int64_t row = (int64_t)bb * p.n_q + hq;
-        float m = p.px_seq_ml[row * 2], l = p.px_seq_ml[row * 2 + 1];
-        const f32x4* po = reinterpret_cast<const f32x4*>(p.px_seq_o + row * D + 8 * c);
-        f32x4 ov[2] = {po[0], po[1]};
-        fold_prefix<T, D, 1, 8>(p, row, 8 * c, m, l, ov);
-        const float inv = l > 0.f ? 1.f / l : 0.f;
-        if (p.lse && c == 0) p.lse[row] = row_lse(m, l);
-        T* o = (T*)p.out + (int64_t)bb * p.o_sb + (int64_t)hq * p.o_sh + 8 * c;
-        store16(o, u32x4{Elem<T>::pack2(ov[0][0] * inv, ov[0][1] * inv), Elem<T>::pack2(ov[0][2] * inv, ov[0][3] * inv),
-                         Elem<T>::pack2(ov[1][0] * inv, ov[1][1] * inv), Elem<T>::pack2(ov[1][2] * inv, ov[1][3] * inv)});
+    if ((int)blockIdx.x >= n_wg) {  // n_fin > 0: shared-prefix cascade
+      const int* rec = p.ws_rec + (int64_t)(blockIdx.x - n_wg) * 8;
+      const int hg = (blockIdx.x - n_wg) % p.n_hgroups;
+      const int c0 = rec[5], c1 = rec[6];
+      if (c0 >= 0) {
+        // shared-prefix cascade: the sequences this range finished (one query token
+        // each), completed with the prefix parts; one thread per (sequence, query head
+        // of the head group, 8 consecutive d). [c0, c1) spans the first and last
+        // sequence the range finished; a sequence between them with no suffix pair
+        // (seq_len == prefix tokens) was skipped by the walker, left no state here, and
+        // is written by its own per-sequence block from the prefix parts alone (its
+        // slot is read here, as every row's is, and not used: the pair count is read
+        // beside the state, one memory round trip for both).
+        constexpr int DV = D / 8;
+        const int hrows = p.hpw * p.n_rep;
+        for (int u = tid; u < (c1 - c0) * hrows * DV; u += blockDim.x) {
+          const int c = u % DV, t = u / DV;
+          const int bb = c0 + t / hrows, hq = hg * hrows + t % hrows;
+          const bool live = decode_pairs(p, bb) != 0;
+          const int64_t row = (int64_t)bb * p.n_q + hq;
+          float m = p.px_seq_ml[row * 2], l = p.px_seq_ml[row * 2 + 1];
+          const f32x4* po = reinterpret_cast<const f32x4*>(p.px_seq_o + row * D + 8 * c);
+          f32x4 ov[2] = {po[0], po[1]};
+          fold_prefix<T, D, 1, 8>(p, row, 8 * c, m, l, ov);
+          if (!live) continue;
+          const float inv = l > 0.f ? 1.f / l : 0.f;
+          if (p.lse && c == 0) p.lse[row] = row_lse(m, l);
+          T* o = (T*)p.out + (int64_t)bb * p.o_sb + (int64_t)hq * p.o_sh + 8 * c;
+          store16(o, u32x4{Elem<T>::pack2(ov[0][0] * inv, ov[0][1] * inv), Elem<T>::pack2(ov[0][2] * inv, ov[0][3] * inv),
+                           Elem<T>::pack2(ov[1][0] * inv, ov[1][1] * inv), Elem<T>::pack2(ov[1][2] * inv, ov[1][3] * inv)});
+        }
       }
+      return;
     }
   }
+  const int* rec = p.ws_rec + (int64_t)blockIdx.x * 8;
+  const int hg = blockIdx.x % p.n_hgroups;
   const int b = rec[0];
   if (b < 0) return;
   const int cb1 = rec[2], slot0 = rec[3], chunk = rec[4];
@@ -1206,7 +1216,7 @@ static int launch_decode_typed(AttnParams p, int max_query_len, char* ws, int64_
   // a shared-prefix merge folds S prefix parts into each of its rows' 8-d pieces (28 x
   // 16 per C4 sequence): 512 threads give every piece its own thread
   const int merge_threads = p.px_n > 0 ? 512 : 256;
-  hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(n_wg + p.batch), dim3(merge_threads), 0, stream, p, n_wg);
+  hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(n_wg + p.batch), dim3(merge_threads), 0, stream, p, n_wg, 0);
   return ss_host::launch_status("paged attention decode merge");
 }
 
@@ -1263,7 +1273,10 @@ static int launch_cascade_typed(const AttnParams& pp, AttnParams ps, int n_pf, c
                          n_pf);
     int st = ss_host::launch_status("shared-prefix cascade");
     if (st != SS_OK) return st;
-    hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(n_wg + ps.batch), dim3(512), 0, stream, ps, n_wg);
+    // blocks: [0, n_wg) split sequences, [n_wg, 2 n_wg) the sequences each range
+    // finished, then one per sequence (rows no other block writes)
+    hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(2 * n_wg + ps.batch), dim3(512), 0, stream, ps, n_wg,
+                       n_wg);
     return ss_host::launch_status("shared-prefix cascade merge");
   }
 }
