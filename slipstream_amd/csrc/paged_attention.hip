@@ -15,6 +15,7 @@ int launch_decode(const AttnParams& p, int dtype, int head_dim, int max_query_le
 int launch_cascade(const AttnParams& pp, const AttnParams& ps, int n_pf, int dtype, int head_dim, char* ws,
                    int64_t ws_bytes, hipStream_t stream);
 int decode_heads_per_wg(int n_kv);
+int64_t cascade_decode_bytes(int dtype, int head_dim, int n_kv, int rmax, int n_ranges);
 int64_t prefill_work_bytes(int64_t batch, int n_rep, int max_query_len);
 int64_t prefill_row_cap(int n_rep, int max_query_len);
 // planned: work already holds the list (count, then (b << 16) | query tile per entry)
@@ -410,9 +411,11 @@ PrefixPlan prefix_plan(int64_t batch, int n_q, int n_kv, int head_dim, int block
   pl.S = (int)((prefix_blocks + cb - 1) / cb);
   const int64_t items = pl.S * per_chunk;
   pl.n_pf = (int)(items < px_wgs ? items : px_wgs);
+  // two decode ranges per workgroup (one per half of its eight waves)
   const int64_t hgroups = n_kv / ss::decode_heads_per_wg(n_kv);
   const int64_t rest = (cus - pl.n_pf) / hgroups;
-  pl.dec_ranges = (int)(rest > 1 ? rest : 1);
+  pl.dec_ranges = 2 * (int)(rest > 1 ? rest : 1);
+  pl.dec = round256(ss::cascade_decode_bytes(dtype, head_dim, n_kv, ss::decode_rows_for(1, n_rep), pl.dec_ranges));
   const int64_t elem = 2;  // bf16 / fp16
   pl.work = 0;  // the prefix pass walks its (chunk, query tile) items in order
   pl.lse = round256(4 * (int64_t)pl.S * batch * n_q);

@@ -549,22 +549,27 @@ __device__ __forceinline__ void load_pair_scalar(const AttnParams& p, const Scal
 // STAB: scalar block-table path (block_size >= 16); otherwise every lane looks up
 // its own block (block_size 4 and 8 put several blocks in one 16-token tile). AUX: the
 // page-load cache policy of the STAB path.
-// The body of decode_kernel as workgroup bid (the shared-prefix cascade runs it in
-// the workgroups after its prefix pass). Waves past hpw (a cascade workgroup has
-// eight, CASCADE) take part in the plan's block reductions and then leave.
+// The body of decode_kernel as workgroup bid. CASCADE: the shared-prefix cascade runs
+// it in the eight-wave workgroups after its prefix pass, each half of the waves
+// (0-3, 4-7) on a range of its own (ranges 2 bid and 2 bid + 1): both halves take
+// part in the plan's block reductions, then waves past hpw in each half leave.
 template <typename T, int D, bool STAB, int AUX, bool CASCADE>
 __device__ __forceinline__ void decode_body(const AttnParams& p, const unsigned bid) {
   typedef DecodeTile<T, D> Tile;
   __shared__ int s_red[16];
-  __shared__ int s_b0, s_c0;
+  __shared__ int s_b0[2], s_c0[2];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave_wg = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = CASCADE ? wave_wg >> 2 : 0;
+  const int wave = CASCADE ? wave_wg & 3 : wave_wg;  // the wave's KV head within its group
+  const unsigned vb = CASCADE ? 2 * bid + half : bid;  // (range, head group) of the wave
   const int n = lane & 15, g = lane >> 4;
-  const int hg = (unsigned)bid % p.n_hgroups;  // unsigned: no sign fix-ups in the division
-  const int wr = (unsigned)bid / p.n_hgroups;
+  const int hg = vb % p.n_hgroups;  // unsigned: no sign fix-ups in the division
+  const int wr = vb / p.n_hgroups;
   const int h = hg * p.hpw + wave;
-  int* rec = p.ws_rec + (int64_t)bid * 8;
+  int* rec = p.ws_rec + (int64_t)vb * 8;
+  const bool rec_writer = CASCADE ? (tid & 255) == 0 : tid == 0;
 
   // ---- plan: total pairs, this range, and the sequence holding its first pair
   // pair count of this thread's first sequence, kept for the scan's first pass (one
@@ -578,31 +583,64 @@ __device__ __forceinline__ void decode_body(const AttnParams& p, const unsigned 
   const int chunk = (total + p.n_ranges - 1) / p.n_ranges;
   const int s_w = wr * chunk;
   const int e_w = min(s_w + chunk, total);
-  if (s_w >= e_w) {
-    if (tid == 0) {
-      rec[0] = -1;
-      rec[5] = -1;
+  if constexpr (!CASCADE) {
+    if (s_w >= e_w) {
+      if (tid == 0) {
+        rec[0] = -1;
+        rec[5] = -1;
+      }
+      return;
     }
-    return;
-  }
-  if (tid == 0) s_b0 = -1;
-  int run = 0;
-  for (int base = 0; base < p.batch; base += blockDim.x) {
-    const int b = base + tid;
-    const int v = base == 0 ? v_first : (b < p.batch ? decode_pairs(p, b) : 0);
-    int tot;
-    const int incl = block_incl_scan(v, s_red, tot);
-    const int cb = run + incl - v;
-    if (v > 0 && cb <= s_w && s_w < cb + v) {
-      s_b0 = b;
-      s_c0 = cb;
+    if (tid == 0) s_b0[0] = -1;
+    int run = 0;
+    for (int base = 0; base < p.batch; base += blockDim.x) {
+      const int b = base + tid;
+      const int v = base == 0 ? v_first : (b < p.batch ? decode_pairs(p, b) : 0);
+      int tot;
+      const int incl = block_incl_scan(v, s_red, tot);
+      const int cb = run + incl - v;
+      if (v > 0 && cb <= s_w && s_w < cb + v) {
+        s_b0[0] = b;
+        s_c0[0] = cb;
+      }
+      run += tot;
+      __syncthreads();
+      if (s_b0[0] >= 0) break;
     }
-    run += tot;
-    __syncthreads();
-    if (s_b0 >= 0) break;
+  } else {
+    // the first pair of both halves' ranges; a half with an empty range is marked
+    // found (-2) from the start, so the scan ends when both are known
+    const int sw2[2] = {(int)((2 * bid) / p.n_hgroups) * chunk, (int)((2 * bid + 1) / p.n_hgroups) * chunk};
+    if (tid < 2) s_b0[tid] = sw2[tid] < min(sw2[tid] + chunk, total) ? -1 : -2;
+    int run = 0;
+    for (int base = 0; base < p.batch; base += blockDim.x) {
+      const int b = base + tid;
+      const int v = base == 0 ? v_first : (b < p.batch ? decode_pairs(p, b) : 0);
+      int tot;
+      const int incl = block_incl_scan(v, s_red, tot);
+      const int cb = run + incl - v;
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        if (v > 0 && cb <= sw2[x] && sw2[x] < cb + v) {
+          s_b0[x] = b;
+          s_c0[x] = cb;
+        }
+      }
+      run += tot;
+      __syncthreads();
+      if (s_b0[0] != -1 && s_b0[1] != -1) break;
+    }
+    // no barrier follows: a half with nothing to do, and waves past hpw, leave here
+    if (s_w >= e_w) {
+      if (rec_writer) {
+        rec[0] = -1;
+        rec[5] = -1;
+      }
+      return;
+    }
+    if (wave >= p.hpw) return;
   }
-  int b = __builtin_amdgcn_readfirstlane(s_b0), c = __builtin_amdgcn_readfirstlane(s_c0), pos = s_w;
-  if (CASCADE && wave >= p.hpw) return;  // no barrier follows
+  int b = __builtin_amdgcn_readfirstlane(s_b0[half]), c = __builtin_amdgcn_readfirstlane(s_c0[half]), pos = s_w;
   // lane byte offsets of the scalar-table path: constant for the whole kernel
   const int tok_bytes = (int)(p.c_so * (int64_t)sizeof(T));
   const int head_bytes = (int)(p.c_sh * (int64_t)sizeof(T));
@@ -644,7 +682,7 @@ __device__ __forceinline__ void decode_body(const AttnParams& p, const unsigned 
         // a sequence finished here, which the merge completes with the prefix parts
         const int slot = c > s_w ? 1 : 0;
         const int64_t pidx = complete ? lse_index(p, b, qoff, j, hq)
-                                      : (((int64_t)bid * 2 + slot) * p.hpw + wave) * p.rmax + n;
+                                      : (((int64_t)vb * 2 + slot) * p.hpw + wave) * p.rmax + n;
         if (row_ok) {
           float* po = (complete ? p.px_seq_o : p.ws_o) + pidx * D;
 #pragma unroll
@@ -889,7 +927,7 @@ __device__ __forceinline__ void decode_body(const AttnParams& p, const unsigned 
       ++b;
     }
   }
-  if (tid == 0) {
+  if (rec_writer) {
     rec[0] = rec_b;
     rec[1] = rec_cb;
     rec[2] = rec_cb1;
@@ -1129,13 +1167,13 @@ struct DecodeGeometry {
   int64_t total() const { return rec_bytes + ml_bytes + o_bytes; }
 };
 
+// n_ranges ranges per head group (0: one workgroup per CU over all head groups)
 template <typename T, int D>
-static DecodeGeometry decode_geometry(int n_kv, int rmax) {
+static DecodeGeometry decode_geometry(int n_kv, int rmax, int n_ranges = 0) {
   DecodeGeometry g;
   g.hpw = heads_per_wg(n_kv);
   g.n_hgroups = n_kv / g.hpw;
-  const int resident = decode_resident_wgs();
-  g.n_ranges = resident / g.n_hgroups;
+  g.n_ranges = n_ranges > 0 ? n_ranges : decode_resident_wgs() / g.n_hgroups;
   if (g.n_ranges < 1) g.n_ranges = 1;
   g.n_wg = g.n_ranges * g.n_hgroups;
   g.rmax = rmax;
@@ -1231,13 +1269,15 @@ static int launch_cascade_typed(const AttnParams& pp, AttnParams ps, int n_pf, c
     ss_host::set_error("shared-prefix cascade: head_dim %d above 128", D);
     return SS_ERR_UNSUPPORTED;
   } else {
-    const DecodeGeometry g = decode_geometry<T, D>(ps.n_kv, decode_rows_for(1, ps.n_rep));
+    // ps.range_cap ranges per head group, two per decode workgroup
+    const DecodeGeometry g = decode_geometry<T, D>(ps.n_kv, decode_rows_for(1, ps.n_rep), ps.range_cap);
     if (ws_bytes < g.total()) {
       ss_host::set_error("shared-prefix cascade: workspace of %lld bytes, decode needs %lld", (long long)ws_bytes,
                          (long long)g.total());
       return SS_ERR_WORKSPACE;
     }
-    if (ps.rmax != g.rmax || ps.block_size < 16 || pp.block_size < 16 || n_pf < 1 || ps.px_n < 1) {
+    if (ps.rmax != g.rmax || ps.block_size < 16 || pp.block_size < 16 || n_pf < 1 || ps.px_n < 1 ||
+        ps.range_cap < 2 || g.n_wg % 2 != 0) {
       ss_host::set_error("shared-prefix cascade: invalid launch (rows %d / %d, block_size %d, %d prefix workgroups)",
                          ps.rmax, g.rmax, ps.block_size, n_pf);
       return SS_ERR_INVALID;
@@ -1248,11 +1288,7 @@ static int launch_cascade_typed(const AttnParams& pp, AttnParams ps, int n_pf, c
     ps.hpw = g.hpw;
     ps.n_hgroups = g.n_hgroups;
     ps.n_ranges = g.n_ranges;
-    int n_wg = g.n_wg;
-    if (ps.range_cap > 0 && ps.n_ranges > ps.range_cap) {
-      ps.n_ranges = ps.range_cap;
-      n_wg = ps.n_ranges * g.n_hgroups;
-    }
+    const int n_wg = g.n_wg;
     const int lds = 6 * TileCfg<T, D>::PLANE;
     const int64_t pool_bytes = 2 * (int64_t)ps.num_blocks * ps.c_sb * (int64_t)sizeof(T);
     const bool nt = pool_bytes > kMallReuseBytes;
@@ -1266,11 +1302,11 @@ static int launch_cascade_typed(const AttnParams& pp, AttnParams ps, int n_pf, c
       attr_set[nt] = true;
     }
     if (nt)
-      hipLaunchKernelGGL((cascade_kernel<T, D, kNonTemporal>), dim3(n_pf + n_wg), dim3(512), lds, stream, pp, ps,
-                         n_pf);
+      hipLaunchKernelGGL((cascade_kernel<T, D, kNonTemporal>), dim3(n_pf + n_wg / 2), dim3(512), lds, stream, pp,
+                         ps, n_pf);
     else
-      hipLaunchKernelGGL((cascade_kernel<T, D, kDefaultPolicy>), dim3(n_pf + n_wg), dim3(512), lds, stream, pp, ps,
-                         n_pf);
+      hipLaunchKernelGGL((cascade_kernel<T, D, kDefaultPolicy>), dim3(n_pf + n_wg / 2), dim3(512), lds, stream, pp,
+                         ps, n_pf);
     int st = ss_host::launch_status("shared-prefix cascade");
     if (st != SS_OK) return st;
     // blocks: [0, n_wg) split sequences, [n_wg, 2 n_wg) the sequences each range
@@ -1304,6 +1340,16 @@ int read_status(int* flags, int clear, hipStream_t stream) {
 }
 
 int decode_heads_per_wg(int n_kv) { return heads_per_wg(n_kv); }
+
+// Bytes of the cascade's decode part: n_ranges ranges per head group.
+int64_t cascade_decode_bytes(int dtype, int head_dim, int n_kv, int rmax, int n_ranges) {
+  if (dtype == SS_DTYPE_BF16) {
+    if (head_dim == 64) return decode_geometry<bf16_t, 64>(n_kv, rmax, n_ranges).total();
+    return decode_geometry<bf16_t, 128>(n_kv, rmax, n_ranges).total();
+  }
+  if (head_dim == 64) return decode_geometry<f16_t, 64>(n_kv, rmax, n_ranges).total();
+  return decode_geometry<f16_t, 128>(n_kv, rmax, n_ranges).total();
+}
 
 int launch_cascade(const AttnParams& pp, const AttnParams& ps, int n_pf, int dtype, int head_dim, char* ws,
                    int64_t ws_bytes, hipStream_t stream) {
