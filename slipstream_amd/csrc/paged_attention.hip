@@ -388,15 +388,14 @@ PrefixPlan prefix_plan(int64_t batch, int n_q, int n_kv, int head_dim, int block
     pl.work = ss::prefill_work_bytes(batch, n_rep, 1);
     return pl;
   }
-  // The prefix pass and the suffix decode run in one launch on disjoint CUs: 7/16 of
+  // The prefix pass and the suffix decode run in one launch on disjoint CUs: 3/8 of
   // them take the prefix chunks (about one item each: items = S * row tiles * n_kv;
-  // chunks hold whole 64-key tiles) and the rest the decode ranges. Each half alone at
-  // C4 (256 CUs): the prefix pass on 84 / 112 / 140 / 168 workgroups 21.9 / 19.4 /
-  // 18.1 / 17.6 us, the suffix decode on 172 / 144 / 128 / 112 ranges 20.6 / 21.1 /
-  // 23.0 / 25.5 us.
+  // chunks hold whole 64-key tiles) and the rest the decode ranges. C4 (256 CUs, 28
+  // items per chunk), whole call in a graph: S = 2 / 3 / 4 / 5 (56 / 84 / 112 / 140
+  // prefix workgroups) 34.4 / 29.3 / 29.6 / 33.2 us.
   const int64_t per_chunk = ((batch * n_rep + 127) / 128) * n_kv;
   const int64_t cus = ss_host::device_cu_count();
-  int64_t px_wgs = cus * 7 / 16;
+  int64_t px_wgs = cus * 3 / 8;
   if (px_wgs < 1) px_wgs = 1;
   int64_t target = px_wgs / per_chunk;
   if (target < 1) target = 1;
