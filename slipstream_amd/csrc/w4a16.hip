@@ -33,6 +33,7 @@
 // Generic path (any other shape, fp32 activations): one thread per output,
 // fp32 dequant and dot product.
 #include <atomic>
+#include <cstdlib>
 
 #include "ss_common.h"
 
@@ -843,6 +844,422 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(2, 2)))
   }
 }
 
+// Eight int4 weights (one word: keys 8j .. 8j + 7 of a row) -> the MFMA B fragment
+// T((q - z) * s) in key order, computed as fma(q, s, -z s) in fp32 and rounded once
+// to the activation type. (The reference rounds (q - z) * s to the scales' dtype and
+// then to the activation dtype, quant_ref.py:112-116,132; with fp16 scales and bf16
+// activations the single rounding differs from that double rounding by at most one
+// bf16 ulp of a weight.) Per word: two masks, eight byte converts (v_cvt_f32_ubyteN),
+// eight FMAs and four packs.
+template <typename T>
+__device__ __forceinline__ u32x4 dequant_word(uint32_t w, float s, float nzs) {
+  // the masks as asm, so that the compiler does not fold each (lo >> 8b) & 0xFF into a
+  // 4-bit field extract and lose the byte converts' own byte select
+  uint32_t lo, hi;
+  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo) : "v"(w));
+  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(hi) : "v"(w >> 4));
+  u32x4 r;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const float qa = (float)((lo >> (8 * b)) & 0xFFu), qb = (float)((hi >> (8 * b)) & 0xFFu);
+    r[b] = Elem<T>::pack2(fmaf(qa, s, nzs), fmaf(qb, s, nzs));
+  }
+  return r;
+}
+
+// Scale of SD (a dtype code) from its raw bits (the low 16 bits for 16-bit scales).
+template <int SD>
+__device__ __forceinline__ float scale_from_bits(uint32_t b) {
+  if constexpr (SD == SS_DTYPE_F16) return (float)__builtin_bit_cast(f16_t, (uint16_t)(b & 0xFFFFu));
+  if constexpr (SD == SS_DTYPE_BF16) return __builtin_bit_cast(float, b << 16);
+  return __builtin_bit_cast(float, b);
+}
+
+constexpr int kWideMT = 8, kWideNS = 2, kWideWV = 8, kWidePF = 4;
+
+// Buffer loads for the wide kernel, written as asm: the compiler inserts no vmcnt wait
+// of its own for them (its count of loads in flight, merged around the loop's back
+// edge, made it wait for nearly every prefetched stage at the top of each stage). The
+// kernel waits itself, with vm_wait_tied, whose register operands keep every use of a
+// loaded value behind the wait. Descriptors are plain SGPR quads over [base, base + bytes):
+// offsets past the end read zeros without a memory access.
+typedef int i32x4w __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4w wide_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  return i32x4w{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xFFFF), (int)bytes, 0x00020000};
+}
+__device__ __forceinline__ u32x4 asm_load_b128_nt(i32x4w rs, int voff, int soff) {
+  u32x4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen nt" : "=v"(v) : "v"(voff), "s"(rs), "s"(soff));
+  return v;
+}
+__device__ __forceinline__ uint32_t asm_load_b32(i32x4w rs, int voff) {
+  uint32_t v;
+  asm volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rs));
+  return v;
+}
+__device__ __forceinline__ uint32_t asm_load_u16(i32x4w rs, int voff) {
+  uint32_t v;
+  asm volatile("buffer_load_ushort %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rs));
+  return v;
+}
+
+// 16 bytes per lane from rs + voff + soff straight into LDS at lds + 16 * lane
+// (buffer_load_dwordx4 ... lds; M0 holds the LDS destination). The s_nop: M0 is
+// written just before by the compiler, and the load may read it one wait state later.
+typedef __attribute__((address_space(3))) char* LdsW;
+__device__ __forceinline__ void asm_dma_b128(i32x4w rs, LdsW lds, int voff, int soff) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)lds;
+  asm volatile("s_nop 1\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(rs), "s"(soff), "{m0}"(m0)
+               : "memory");
+}
+
+// s_waitcnt vmcnt(N) with the registers of one stage's weight loads as operands, so
+// that no use of them is scheduled above the wait.
+template <int N, int NS>
+__device__ __forceinline__ void vm_wait_tied(u32x4 (&w)[NS]) {
+  static_assert(NS == 2 || NS == 4, "operand lists for two or four weight tiles");
+  static_assert(N == 0 || N == NS, "wait counts used by the wide kernel");
+  if constexpr (NS == 4) {
+    if constexpr (N == 0)
+      asm volatile("s_waitcnt vmcnt(0)" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]) : : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(4)" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]) : : "memory");
+  } else {
+    if constexpr (N == 0)
+      asm volatile("s_waitcnt vmcnt(0)" : "+v"(w[0]), "+v"(w[1]) : : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(2)" : "+v"(w[0]), "+v"(w[1]) : : "memory");
+  }
+}
+
+// Wide kernel (w4a16_wide_kernel, m > 64 and g == 128): the weights dequantised once
+// per wave into bf16/fp16 MFMA operands, each serving a whole 128-row activation tile.
+// Workgroup: four waves, 16*MT activation rows x 64*NS weight rows; wave w owns the
+// weight rows [nb + 16 NS w, + 16 NS) against every activation row of the tile, so no
+// weight is dequantised twice inside a workgroup. Per 128-key stage (one quantisation
+// group):
+//   - each lane loads its 32 keys of each of its NS weight rows (one 16-byte load per
+//     16-row tile, four lanes reading a row's 64 contiguous bytes) PF stages ahead (a
+//     register ring; loads past the range use an offset past every operand and return
+//     zeros without a memory access), and turns each 8-key word into the B fragment
+//     T((q - z) s) in registers (dequant_word); every fragment then feeds MT MFMAs.
+//     There is no per-group fold on the accumulators and no activation row sums: the
+//     scale is inside the operand. The (s, -z s) pairs of the workgroup's rows and
+//     range sit in an LDS table filled once (per-stage scale and zero-point loads, 16
+//     rows per instruction, cost about a fifth of the time).
+//   - the activation stage (16*MT rows x 128 keys) goes straight into LDS by DMA
+//     (buffer_load ... lds: lane l of an instruction writes 16 bytes at 16 l), double
+//     buffered with one barrier per stage: an instruction brings four whole rows
+//     (256 bytes each), 16-byte chunk c of row r at position c ^ (r % 16) of the row,
+//     so that the MFMA A-fragment reads (lane m of a 16-lane group: row m, one chunk)
+//     hit sixteen distinct positions: no bank conflicts. Stage i + 2 is requested right
+//     after the barrier that ends stage i.
+//   - one explicit wait per stage (before that barrier): the loads are asm, issued in a
+//     fixed order (stage i: the weights of stage i + PF, then after the barrier the
+//     activations of stage i + 2), so the wait for the next activation stage (everything
+//     but the NS weight loads just issued) also covers the next stage's weights.
+//   - inside a stage, the fragment reads and the dequantisation of key step s + 1 are
+//     issued before the MFMAs of step s (two register sets).
+//   - results through LDS (the activation buffers) as 16-byte row chunks: the output in
+//     T, or with ranges > 1 fp32 partials [ks][m][n] that w4a16_splitk_reduce_kernel
+//     adds in range order.
+// Per stage and wave (MT = 8): 32 NS MFMAs, 4 NS words dequantised (about 23 VALU
+// instructions each) and 32 fragment reads.
+template <typename T, int MT, int NS, int WV, int SD>
+__global__ __launch_bounds__(64 * WV) void w4a16_wide_kernel(const W4Params p, float* __restrict__ part,
+                                                             unsigned long long* __restrict__ arrivals,
+                                                             unsigned long long tag, int kchunk, int ks, int n_tiles,
+                                                             int m_blocks) {
+  constexpr int PF = kWidePF;     // weight stages in flight while one computes
+  constexpr int NTHR = 64 * WV;   // threads
+  constexpr int BM = 16 * MT;     // activation rows of the workgroup
+  constexpr int TR = 16 * NS * WV;  // weight rows of the workgroup
+  constexpr int XBYTES = BM * 256;  // one activation stage
+  constexpr int XI = BM / (4 * WV);  // DMA instructions per wave and stage (four rows each)
+  static_assert(XI * 4 * WV == BM, "whole DMA instructions per wave");
+  constexpr int ESZ = SD == SS_DTYPE_F32 ? 4 : 2;
+  static_assert(PF % 2 == 0, "stage i + u reads activation buffer u & 1");
+  extern __shared__ __attribute__((aligned(16))) char s_dyn[];
+  float2* const s_tab = reinterpret_cast<float2*>(s_dyn + 2 * XBYTES);  // [stage of the range][TR]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ln = lane & 15, kg = lane >> 4;
+  // workgroup -> (K range, weight tile, activation block), the activation blocks of one
+  // (range, weight tile) pair 8 ids apart so that they share an XCD and its L2 (the
+  // workgroups go round robin over the eight XCDs); ids past the last pair exit
+  const int blk = blockIdx.x / (8 * m_blocks), within = blockIdx.x - blk * 8 * m_blocks;
+  const int pair = blk * 8 + (within & 7);
+  if (pair >= ks * n_tiles) return;
+  const int zr = pair % ks;
+  const int nb = (pair / ks) * TR;
+  const int n0 = nb + wave * 16 * NS;
+  const int m0 = (within >> 3) * BM;
+  const int rows = min(BM, p.m - m0);
+  const int i0 = zr * kchunk;
+  const int i1 = min(p.k >> 7, i0 + kchunk);
+  const int nst = i1 - i0;
+
+  // ---- weights: rows past N repeat row N - 1 (never stored)
+  const i32x4w rw = wide_rsrc(p.qw, (uint32_t)((int64_t)p.n * p.k / 2));
+  int w_off[NS];
+#pragma unroll
+  for (int ns = 0; ns < NS; ++ns) w_off[ns] = min(n0 + ns * 16 + ln, p.n - 1) * (p.k / 2) + 16 * kg;
+  u32x4 wr[PF][NS];
+  auto load_w = [&](int i, u32x4 (&w)[NS]) {
+    const int so = __builtin_amdgcn_readfirstlane(i < i1 ? i * 64 : kOutOfRange);
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) w[ns] = asm_load_b128_nt(rw, w_off[ns], so);
+  };
+
+  // ---- activations: DMA instruction u of wave w brings rows 4 (XI w + u) + l / 16 of
+  // the stage, lane l the chunk (l % 16) ^ (row % 16); rows past M read row M - 1 (their
+  // outputs are never stored)
+  const i32x4w rx = wide_rsrc((const T*)p.x + (int64_t)m0 * p.x_stride,
+                              (uint32_t)(((int64_t)(rows - 1) * p.x_stride + p.k) * sizeof(T)));
+  int x_off[XI];
+#pragma unroll
+  for (int u = 0; u < XI; ++u) {
+    const int r = 4 * (XI * wave + u) + kg;
+    x_off[u] = (int)((int64_t)min(r, rows - 1) * p.x_stride * (int64_t)sizeof(T)) + 16 * (ln ^ (r & 15));
+  }
+  const LdsW lds_x = (LdsW)s_dyn;
+  auto dma_x = [&](int i, int buf) {
+    const int so = __builtin_amdgcn_readfirstlane(i < i1 ? i * 128 * (int)sizeof(T) : kOutOfRange);
+#pragma unroll
+    for (int u = 0; u < XI; ++u) asm_dma_b128(rx, lds_x + buf * XBYTES + (XI * wave + u) * 1024, x_off[u], so);
+  };
+  // A fragment (tile mt, key step s) of lane (ln, kg): row 16 mt + ln, keys 32 kg + 8 s
+  // (the keys of the weight word the lane's B fragment holds in step s), i.e. chunk
+  // 4 kg + s of the row, at position (4 kg + s) ^ ln
+  int a_off[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) a_off[s] = (ln >> 2) * 1024 + (ln & 3) * 256 + 16 * ((4 * kg + s) ^ ln);
+
+  // ---- the (s, -z s) table of the workgroup's rows over the range's stages, in
+  // batches of TB entries per thread; the first batch is requested before the weight and
+  // activation prologue, so their latencies overlap
+  constexpr int TB = 16;
+  const i32x4w rsc = wide_rsrc(p.sc, (uint32_t)((int64_t)p.n * p.groups * ESZ));
+  const i32x4w rzp = wide_rsrc(p.qz, (uint32_t)((int64_t)p.n * p.groups * 4));
+  const int total = TR * nst;
+  uint32_t sb[TB], zb[TB];
+  auto table_load = [&](int q0) {
+#pragma unroll
+    for (int j = 0; j < TB; ++j) {  // entry q: row q / nst, stage q % nst (groups contiguous)
+      const int q = min(q0 + NTHR * j + (int)threadIdx.x, total - 1);
+      const int r = q / nst, gl = q - r * nst;
+      const int gi = min(nb + r, p.n - 1) * p.groups + i0 + gl;
+      sb[j] = ESZ == 2 ? asm_load_u16(rsc, gi * 2) : asm_load_b32(rsc, gi * 4);
+      zb[j] = asm_load_b32(rzp, gi * 4);
+    }
+  };
+  auto table_tie = [&]() {  // no use of the batch above the preceding wait
+    asm volatile("" : "+v"(sb[0]), "+v"(sb[1]), "+v"(sb[2]), "+v"(sb[3]), "+v"(sb[4]), "+v"(sb[5]), "+v"(sb[6]),
+                 "+v"(sb[7]), "+v"(sb[8]), "+v"(sb[9]), "+v"(sb[10]), "+v"(sb[11]), "+v"(sb[12]), "+v"(sb[13]),
+                 "+v"(sb[14]), "+v"(sb[15]));
+    asm volatile("" : "+v"(zb[0]), "+v"(zb[1]), "+v"(zb[2]), "+v"(zb[3]), "+v"(zb[4]), "+v"(zb[5]), "+v"(zb[6]),
+                 "+v"(zb[7]), "+v"(zb[8]), "+v"(zb[9]), "+v"(zb[10]), "+v"(zb[11]), "+v"(zb[12]), "+v"(zb[13]),
+                 "+v"(zb[14]), "+v"(zb[15]));
+  };
+  auto table_store = [&](int q0) {
+#pragma unroll
+    for (int j = 0; j < TB; ++j) {
+      const int q = q0 + NTHR * j + (int)threadIdx.x;
+      if (q < total) {
+        const int r = q / nst, gl = q - r * nst;
+        const float sc = scale_from_bits<SD>(sb[j]);
+        s_tab[gl * TR + r] = float2{sc, -sc * (float)(int)zb[j]};
+      }
+    }
+  };
+
+  f32x4 acc[MT][NS];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) acc[mt][ns] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // One stage: key step s multiplies the fragments read during step s - 1 with the B
+  // operands dequantised during step s - 1, while the next step's fragments are read
+  // and its weights dequantised.
+  auto compute = [&](int i, int buf, const u32x4 (&w)[NS]) {
+    float sc[NS], nzs[NS];
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) {
+      const float2 t = s_tab[(i - i0) * TR + wave * 16 * NS + 16 * ns + ln];
+      sc[ns] = t.x;
+      nzs[ns] = t.y;
+    }
+    const char* const xs = (const char*)s_dyn + buf * XBYTES;
+    u32x4 a[2][MT], b[2][NS];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) a[0][mt] = *reinterpret_cast<const u32x4*>(xs + mt * 4096 + a_off[0]);
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) b[0][ns] = dequant_word<T>(w[ns][0], sc[ns], nzs[ns]);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int c = s & 1;
+      if (s < 3) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          a[c ^ 1][mt] = *reinterpret_cast<const u32x4*>(xs + mt * 4096 + a_off[s + 1]);
+#pragma unroll
+        for (int ns = 0; ns < NS; ++ns) b[c ^ 1][ns] = dequant_word<T>(w[ns][s + 1], sc[ns], nzs[ns]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ns = 0; ns < NS; ++ns) acc[mt][ns] = Elem<T>::mfma(a[c][mt], b[c][ns], acc[mt][ns]);
+    }
+    // One wave per SIMD: the next step's fragment reads and dequantisation only overlap
+    // the MFMAs if they are issued between them (in order, a VALU instruction issues
+    // while the matrix core works on the MFMA before it). Per step: MT * NS MFMAs, each
+    // followed by three VALU instructions, a fragment read before every NS MFMAs.
+#pragma unroll
+    for (int s = 0; s < 3; ++s)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+#pragma unroll
+        for (int ns = 0; ns < NS; ++ns) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+        }
+      }
+  };
+
+  // prologue: the first table batch, PF weight stages and the first two activation
+  // stages requested; all but the second activation stage landed, the table stored
+  asm volatile("s_nop 4");  // descriptor SGPRs written by VALU (readfirstlane) before the first load
+  table_load(0);
+#pragma unroll
+  for (int u = 0; u < PF; ++u) load_w(i0 + u, wr[u]);
+  dma_x(i0, 0);
+  dma_x(i0 + 1, 1);
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(XI) : "memory");
+  table_tie();
+  vm_wait_tied<0, NS>(wr[0]);  // (no-op by now: register operands only)
+  table_store(0);
+  for (int q0 = NTHR * TB; q0 < total; q0 += NTHR * TB) {  // tables of more than one batch
+    table_load(q0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    table_tie();
+    table_store(q0);
+  }
+  __syncthreads();
+  // every range is a whole number of PF stages (host-checked): no branch in the body,
+  // which keeps the accumulators in place across the unrolled stages. Stage j reads
+  // activation buffer j & 1 (i0 is a multiple of PF, PF is even).
+  for (int i = i0; i < i1; i += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      compute(i + u, u & 1, wr[u]);
+      load_w(i + u + PF, wr[u]);
+      // the activations of stage i + u + 1 (requested before the NS weight loads just
+      // issued) and, older, the weights of stage i + u + 1 have landed
+      vm_wait_tied<NS, NS>(wr[(u + 1) % PF]);
+      __syncthreads();  // every wave's part of stage i + u + 1 is in LDS; buffer u & 1 is free
+      dma_x(i + u + 2, u & 1);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // prefetches past the range
+  __syncthreads();  // the activation buffers are free for the results
+
+  // ---- results through LDS in passes of MTP activation tiles: lane holds
+  // C[m0 + 16 mt + 4 kg + e][n0 + 16 ns + ln]; each thread then writes 16-byte row chunks
+  constexpr int PITCH = TR + 4;  // floats per LDS row (skewed)
+  constexpr int PR = (2 * XBYTES / 4) / PITCH / 16 * 16;
+  constexpr int MTP = PR / 16 >= MT ? MT : (PR / 16 >= 4 ? 4 : (PR / 16 >= 2 ? 2 : 1));
+  static_assert(PR >= 16 && MT % MTP == 0, "whole passes");
+  float* const s_t = reinterpret_cast<float*>(s_dyn);
+  const bool split = ks > 1;
+  const bool vec_n = p.n % 4 == 0;
+  const bool vec_out = vec_n && p.o_stride % 4 == 0 && ((uintptr_t)p.out & 7) == 0;
+  // two ranges with arrival words (N % 4 == 0): partials stored at device scope, and the
+  // second range to finish a tile adds both (below) instead of a second kernel
+  const bool fused = ks == 2 && arrivals != nullptr;
+  const __amdgpu_buffer_rsrc_t rp =
+      buffer_rsrc(part + ((int64_t)zr * p.m + m0) * p.n, (uint32_t)((int64_t)rows * p.n * 4));
+#pragma unroll
+  for (int mt0 = 0; mt0 < MT; mt0 += MTP) {
+    if (mt0 > 0) __syncthreads();  // the previous pass has been read
+#pragma unroll
+    for (int mt = mt0; mt < mt0 + MTP; ++mt)
+#pragma unroll
+      for (int ns = 0; ns < NS; ++ns)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          s_t[(16 * (mt - mt0) + 4 * kg + e) * PITCH + wave * 16 * NS + 16 * ns + ln] = acc[mt][ns][e];
+    __syncthreads();
+    for (int q = threadIdx.x; q < 16 * MTP * (TR / 4); q += NTHR) {
+      const int rl = q / (TR / 4), c4 = q - rl * (TR / 4);
+      const int m = m0 + 16 * mt0 + rl, n = nb + 4 * c4;
+      if (m >= p.m || n >= p.n) continue;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&s_t[rl * PITCH + 4 * c4]);
+      if (fused) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp, ((m - m0) * p.n + n) * 4, 0,
+                                               kDeviceScope);
+      } else if (split) {
+        float* const dst = part + ((int64_t)zr * p.m + m) * p.n + n;
+        if (vec_n) {
+          *reinterpret_cast<f32x4*>(dst) = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < p.n) dst[e] = v[e];
+        }
+      } else {
+        T* const o = (T*)p.out + (int64_t)m * p.o_stride + n;
+        if (vec_out) {
+          const T h[4] = {(T)v[0], (T)v[1], (T)v[2], (T)v[3]};
+          *reinterpret_cast<u32x2*>(o) = __builtin_bit_cast(u32x2, h);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < p.n) o[e] = (T)v[e];
+        }
+      }
+    }
+  }
+  if (!fused) return;
+
+  // Two ranges: the second to arrive at the tile reads both ranges' partials (device
+  // scope: the other range's came from another CU, possibly another XCD) and writes
+  // (0 + p0) + p1, the reduce kernel's sums in its order, whichever range arrives last
+  __shared__ int s_last;
+  wait_vm0();       // this thread's partials have reached the point of device coherence
+  __syncthreads();  // every thread's, before the count moves
+  if (threadIdx.x == 0) s_last = arrive_last(arrivals + (pair / ks) * m_blocks + (within >> 3), tag, ks) ? 1 : 0;
+  __syncthreads();
+  if (!s_last) return;
+  const __amdgpu_buffer_rsrc_t r0 = buffer_rsrc(part + (int64_t)m0 * p.n, (uint32_t)((int64_t)rows * p.n * 4));
+  const __amdgpu_buffer_rsrc_t r1 =
+      buffer_rsrc(part + ((int64_t)p.m + m0) * p.n, (uint32_t)((int64_t)rows * p.n * 4));
+  for (int q = threadIdx.x; q < BM * (TR / 4); q += NTHR) {
+    const int rl = q / (TR / 4), c4 = q - rl * (TR / 4);
+    const int m = m0 + rl, n = nb + 4 * c4;
+    if (m >= p.m || n >= p.n) continue;
+    const int off = (rl * p.n + n) * 4;
+    const f32x4 p0 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r0, off, 0, kDeviceScope));
+    const f32x4 p1 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r1, off, 0, kDeviceScope));
+    f32x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = (0.f + p0[e]) + p1[e];
+    T* const o = (T*)p.out + (int64_t)m * p.o_stride + n;
+    if (vec_out) {
+      const T h[4] = {(T)y[0], (T)y[1], (T)y[2], (T)y[3]};
+      *reinterpret_cast<u32x2*>(o) = __builtin_bit_cast(u32x2, h);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (T)y[e];  // N % 4 == 0: the chunk is whole
+    }
+  }
+}
+
 // Skinny kernel (2 <= m <= 16, and up to m = 64 for 4096 x 4096, g == 128): bandwidth-
 // bound shapes without a K split across workgroups. A workgroup owns 16*NS weight rows and KW waves; wave w takes the
 // 128*ST keys [w*128*ST, (w+1)*128*ST) of those rows and of the 16*MT activation rows,
@@ -1410,6 +1827,7 @@ struct W4Plan {
   int gemv;  // 1: the batch-1 GEMV kernel
   bool tile;  // the tiled kernel (activations shared through LDS)
   bool skinny;  // the skinny kernel (m <= 64, K split over the waves of one workgroup)
+  bool widek;   // the wide kernel (m > 64, weights dequantised once per wave)
   int st;       // skinny: 128-key stages per wave
   int mt, ns, bit, kw, pf;
   int m_blocks, n_tiles;
@@ -1563,9 +1981,55 @@ bool plan_skinny(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
 
 // Split-K workspace of the tiled kernel: the fp32 partials [ranges][m][n], then (256-byte
 // aligned) one 64-bit arrival word per output tile (weight tile x activation block).
+// The wide kernel's: the partials alone.
 int64_t tile_part_bytes(const W4Plan& pl, int64_t m, int64_t n) { return ((int64_t)pl.ks * m * n * 4 + 255) / 256 * 256; }
 int64_t tile_workspace_bytes(const W4Plan& pl, int64_t m, int64_t n) {
+  if (pl.widek) return pl.ks > 1 ? tile_part_bytes(pl, m, n) + (int64_t)pl.n_tiles * pl.m_blocks * 8 : 0;
   return pl.tile && pl.ks > 1 ? tile_part_bytes(pl, m, n) + (int64_t)pl.n_tiles * pl.m_blocks * 8 : 0;
+}
+
+// Wide kernel for m > 64 with g == 128: 128 x 256 workgroup tiles, K split over
+// workgroups so that the grid holds about one workgroup per CU (the kernel's 64 KB of
+// activation stages and its registers allow one per CU), in ranges of equal length of
+// at least two stages.
+constexpr size_t kWideXLds = (size_t)2 * kWideMT * 16 * 256;  // two activation stages
+constexpr size_t kWideLdsMax = 160 * 1024 - 256;  // the CU's LDS less the kernel's static bytes
+size_t wide_lds_bytes(int ns, int kchunk) { return kWideXLds + (size_t)16 * ns * kWideWV * kchunk * 8; }
+
+bool plan_wide(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
+  if (!pl.wide || m <= 64 || g != 128) return false;
+  static const int enabled = [] {
+    const char* e = getenv("SLIPSTREAM_W4A16_WIDE");
+    return e ? atoi(e) : 1;
+  }();
+  if (!enabled) return false;
+  const int64_t stages = k / 128;
+  if (stages % kWidePF) return false;  // ranges of whole PF-stage rounds
+  const int64_t n_tiles = (n + 16 * kWideNS * kWideWV - 1) / (16 * kWideNS * kWideWV);
+  const int64_t m_blocks = (m + 16 * kWideMT - 1) / (16 * kWideMT);
+  if (n_tiles > 65535 || m_blocks > 65535) return false;
+  const int64_t tiles = n_tiles * m_blocks;
+  const int64_t target = ss_host::device_cu_count();
+  int64_t ks = (target + tiles / 2) / tiles;
+  const int64_t rounds = stages / kWidePF;
+  ks = ks < 1 ? 1 : (ks > rounds ? rounds : ks);
+  int64_t per = (rounds + ks - 1) / ks * kWidePF;  // stages per range
+  while (per > kWidePF && wide_lds_bytes(kWideNS, (int)per) > kWideLdsMax) per -= kWidePF;  // the table fits
+  if (wide_lds_bytes(kWideNS, (int)per) > kWideLdsMax) return false;
+  // short ranges leave the per-workgroup set-up and result traffic uncovered: below 12
+  // stages the tiled kernel is faster (C5 at m = 256: 4096 x 6144 in 4 ranges of 8 stages
+  // 36.6 against 31.8 us, 4096 x 4096 in 8 ranges of 4 stages 32.3 against 22.0 us)
+  if (per < 12) return false;
+  ks = (stages + per - 1) / per;
+  if (ks > 65535) return false;
+  pl.widek = true;
+  pl.mt = kWideMT, pl.ns = kWideNS;
+  pl.n_tiles = (int)n_tiles;
+  pl.m_blocks = (int)m_blocks;
+  pl.ks = (int)ks;
+  pl.kchunk = (int)per;
+  pl.lds = wide_lds_bytes(kWideNS, (int)per);
+  return true;
 }
 
 constexpr size_t kLdsBudget = 64 * 1024;  // LDS bytes per workgroup
@@ -1600,6 +2064,8 @@ W4Plan plan_w4a16(int64_t m, int64_t n, int64_t k, int g, bool act16, bool allow
     }
   }
   if (plan_skinny(pl, m, n, k, g)) return pl;
+  if (allow_tile && plan_wide(pl, m, n, k, g)) return pl;
+  pl.widek = false;
   if (allow_tile && plan_tile(pl, m, n, k, g)) return pl;
   pl.tile = false;
   const size_t unit = pl.wide ? 128 : 32;
@@ -1801,8 +2267,52 @@ int launch_w4a16_narrow_mr(const W4Params& p, const W4Plan& pl, hipStream_t stre
   return launch_w4a16_narrow_sd<T, MR, SS_DTYPE_F32>(p, pl, stream);
 }
 
+template <typename T, int SD>
+int launch_w4a16_wide_sd(const W4Params& p, const W4Plan& pl, float* part, hipStream_t stream) {
+  auto kern = w4a16_wide_kernel<T, kWideMT, kWideNS, kWideWV, SD>;
+  static bool attr_set = false;  // per instantiation; the attribute is process-wide
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLdsMax) !=
+        hipSuccess) {
+      ss_host::set_error("w4a16 gemm: cannot reserve %d bytes of LDS", (int)kWideLdsMax);
+      return SS_ERR_UNSUPPORTED;
+    }
+    attr_set = true;
+  }
+  const int64_t pairs = (int64_t)pl.ks * pl.n_tiles;
+  const int64_t grid = (pairs + 7) / 8 * 8 * pl.m_blocks;
+  if (grid > 0x7fffffff || pl.lds != wide_lds_bytes(kWideNS, pl.kchunk) || pl.kchunk % kWidePF) {
+    ss_host::set_error("w4a16 gemm: wide plan of %lld workgroups, %zu LDS bytes", (long long)grid, pl.lds);
+    return SS_ERR_UNSUPPORTED;
+  }
+  // two ranges (whole 16-byte row chunks, N % 4 == 0): the second range to finish a tile
+  // adds the partials itself (C5 gate at m = 256: no reduce launch)
+  const bool fused = pl.ks == 2 && p.n % 4 == 0;
+  unsigned long long* const arrivals = fused ? (unsigned long long*)((char*)part + tile_part_bytes(pl, p.m, p.n)) : nullptr;
+  const unsigned long long tag = fused ? next_arrival_tag() : 0ull;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * kWideWV), pl.lds, stream, p, part, arrivals, tag, pl.kchunk,
+                     pl.ks, pl.n_tiles, pl.m_blocks);
+  int st = ss_host::launch_status("w4a16 gemm (wide)");
+  if (st != SS_OK || pl.ks == 1 || fused) return st;
+  const bool vec = p.n % 4 == 0;
+  const int64_t threads = (int64_t)p.m * (vec ? p.n / 4 : p.n);
+  const unsigned blocks = (unsigned)((threads + 255) / 256);
+  if (vec)
+    hipLaunchKernelGGL((w4a16_splitk_reduce_kernel<T, 4>), dim3(blocks), dim3(256), 0, stream, part, p.out, p.m, p.n,
+                       pl.ks, p.o_stride);
+  else
+    hipLaunchKernelGGL((w4a16_splitk_reduce_kernel<T, 1>), dim3(blocks), dim3(256), 0, stream, part, p.out, p.m, p.n,
+                       pl.ks, p.o_stride);
+  return ss_host::launch_status("w4a16 split-K reduce");
+}
+
 template <typename T>
 int launch_w4a16_typed(const W4Params& p, const W4Plan& pl, float* part, hipStream_t stream) {
+  if (pl.widek) {
+    if (p.sdt == SS_DTYPE_F16) return launch_w4a16_wide_sd<T, SS_DTYPE_F16>(p, pl, part, stream);
+    if (p.sdt == SS_DTYPE_BF16) return launch_w4a16_wide_sd<T, SS_DTYPE_BF16>(p, pl, part, stream);
+    return launch_w4a16_wide_sd<T, SS_DTYPE_F32>(p, pl, part, stream);
+  }
   if (pl.narrow == 1) return launch_w4a16_narrow_mr<T, 1>(p, pl, stream);
   if (pl.narrow == 2) return launch_w4a16_narrow_mr<T, 2>(p, pl, stream);
   if (pl.narrow == 4) return launch_w4a16_narrow_mr<T, 4>(p, pl, stream);
@@ -1924,7 +2434,7 @@ extern "C" int ss_w4a16_gemm(const void* x, void* out, const int32_t* qweight, c
   if (pl.fast && ((int64_t)63 * x_stride + k) * 2 >= ((int64_t)1 << 31)) pl.fast = false;
   // scale and zero-point offsets are 32-bit byte offsets
   if (pl.fast && n * (k / group_size) * 4 >= ((int64_t)1 << 31)) pl.fast = false;
-  if (pl.fast && pl.tile && pl.ks > 1) {
+  if (pl.fast && (pl.tile || pl.widek) && pl.ks > 1) {
     // the K split needs the workspace ss_w4a16_workspace_size reports; without it
     // (or unaligned) the untiled MFMA kernel runs, which needs none
     const int64_t need = ss::tile_workspace_bytes(pl, m, n);

@@ -211,6 +211,63 @@ def test_tiled_two_ranges_finished_in_kernel(device, m, n, act, sdt):
         assert torch.equal(again, y)
 
 
+# (plans as the host computes them for 256 CUs: 128 x 256 workgroup tiles, ranges of a
+# multiple of 4 stages and at least 12)
+@pytest.mark.parametrize("m,k,n,act,sdt", [
+    (300, 2048, 16000, torch.float16, torch.bfloat16),   # one range; 3 M blocks (the last of 44 rows), a half last weight tile
+    (256, 3072, 16384, torch.bfloat16, torch.float16),   # two ranges of 12 stages, finished in the kernel
+    (256, 4096, 12800, torch.bfloat16, torch.float32),   # three ranges (12, 12, 8 stages) and the reduce kernel
+    (256, 3072, 16382, torch.bfloat16, torch.float16),   # two ranges, N % 4 != 0: partials and the reduce kernel
+])
+def test_wide_kernel(device, m, k, n, act, sdt):
+    """The wide kernel (m > 64, g = 128: weights dequantised once per wave with the scale
+    inside the operand, 128 x 256 workgroup tiles, activations by DMA into LDS): ragged M
+    and N, one, two and three K ranges, every scale dtype, random zero points. Within the
+    tolerance of the float64 oracle and bit-identical across repeats."""
+    print(f"w4a16 wide m={m} k={k} n={n} {act} {sdt}", flush=True)
+    x, qw, s, z, ref = _host_case(n, k, m, 128, seed=m + k + n, act=act, sdt=sdt, zeros="random")
+    xd, qd, sd, zd = x.to(device), qw.to(device), s.to(device), z.to(device)
+    y = w4a16_gemm(xd, qd, sd, zd, 128)
+    assert y.dtype == act
+    _assert_close(y, ref, f"wide m={m} k={k} n={n}")
+    assert torch.equal(y, w4a16_gemm(xd, qd, sd, zd, 128))
+
+
+def test_wide_kernel_two_ranges_graph_and_dirty_workspace(device):
+    """The wide kernel's in-kernel finish of two K ranges (arrival words behind the
+    partials, tagged per call): correct on a workspace full of 0xFF bytes and replayed
+    from a captured graph (one tag for every replay) to the eager result, with eager
+    calls in between."""
+    from slipstream_amd.kernels import quant_gemm
+    x, qw, s, z, ref = _host_case(16384, 3072, 256, 128, seed=77, zeros="random")
+    xd, qd, sd, zd = x.to(device), qw.to(device), s.to(device), z.to(device)
+    y = w4a16_gemm(xd, qd, sd, zd, 128)
+    _assert_close(y, ref, "wide two ranges")
+    torch.cuda.synchronize()
+    for ws in quant_gemm._WORKSPACE.values():
+        ws.fill_(0xFF)
+    y1 = w4a16_gemm(xd, qd, sd, zd, 128)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        w4a16_gemm(xd, qd, sd, zd, 128)
+    st.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        out = w4a16_gemm(xd, qd, sd, zd, 128)
+    for rep in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y), f"replay {rep}"
+        again = w4a16_gemm(xd, qd, sd, zd, 128)
+        torch.cuda.synchronize()
+        assert torch.equal(again, y)
+
+
 def test_tiled_uneven_ranges_from_the_table_cap(device):
     """K = 15360 at M = 40 over 258 weight tiles: one range per tile would need a 122 KB
     scale table, so the host splits K until a range's table fits 40 KB -- 4 ranges of 32,
