@@ -920,19 +920,14 @@ __device__ __forceinline__ void asm_dma_b128(i32x4w rs, LdsW lds, int voff, int 
 // that no use of them is scheduled above the wait.
 template <int N, int NS>
 __device__ __forceinline__ void vm_wait_tied(u32x4 (&w)[NS]) {
-  static_assert(NS == 2 || NS == 4, "operand lists for two or four weight tiles");
-  static_assert(N == 0 || N == NS, "wait counts used by the wide kernel");
-  if constexpr (NS == 4) {
-    if constexpr (N == 0)
-      asm volatile("s_waitcnt vmcnt(0)" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]) : : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(4)" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]) : : "memory");
-  } else {
-    if constexpr (N == 0)
-      asm volatile("s_waitcnt vmcnt(0)" : "+v"(w[0]), "+v"(w[1]) : : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(2)" : "+v"(w[0]), "+v"(w[1]) : : "memory");
-  }
+  static_assert(NS == 1 || NS == 2 || NS == 4, "operand lists for one, two or four weight tiles");
+  static_assert(N >= 0 && N < 16, "vmcnt range of the encoding used");
+  if constexpr (NS == 4)
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]) : "n"(N) : "memory");
+  else if constexpr (NS == 2)
+    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(w[0]), "+v"(w[1]) : "n"(N) : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(%1)" : "+v"(w[0]) : "n"(N) : "memory");
 }
 
 // Wide kernel (w4a16_wide_kernel, m > 64 and g == 128): the weights dequantised once
@@ -1989,9 +1984,10 @@ int64_t tile_workspace_bytes(const W4Plan& pl, int64_t m, int64_t n) {
 }
 
 // Wide kernel for m > 64 with g == 128: 128 x 256 workgroup tiles, K split over
-// workgroups so that the grid holds about one workgroup per CU (the kernel's 64 KB of
-// activation stages and its registers allow one per CU), in ranges of equal length of
-// at least two stages.
+// workgroups so that the grid holds about one workgroup per CU (the kernel's eight waves
+// and its LDS allow one per CU), in ranges of equal length of at least 12 stages. (A
+// 64 x 256 form for 16 < m <= 64 measured no faster than the tiled kernel: 4096 x 28672
+// at m = 64 37.1 against 35.4 us.)
 constexpr size_t kWideXLds = (size_t)2 * kWideMT * 16 * 256;  // two activation stages
 constexpr size_t kWideLdsMax = 160 * 1024 - 256;  // the CU's LDS less the kernel's static bytes
 size_t wide_lds_bytes(int ns, int kchunk) { return kWideXLds + (size_t)16 * ns * kWideWV * kchunk * 8; }
@@ -2005,8 +2001,14 @@ bool plan_wide(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
   if (!enabled) return false;
   const int64_t stages = k / 128;
   if (stages % kWidePF) return false;  // ranges of whole PF-stage rounds
-  const int64_t n_tiles = (n + 16 * kWideNS * kWideWV - 1) / (16 * kWideNS * kWideWV);
   const int64_t m_blocks = (m + 16 * kWideMT - 1) / (16 * kWideMT);
+  // 256 weight rows per workgroup (two 16-row tiles a wave), or 128 (one) where 256-row
+  // tiles would leave the grid under three quarters of the CUs before any K split (C5 at
+  // m = 256: 4096 x 14336 unsplit on 128-row tiles 51.1 us, in two ranges on 256-row
+  // tiles 53.6 us; the stacked 4096 x 28672 stays on 256-row tiles, unsplit, 78.5 us)
+  int ns = kWideNS;
+  if ((n + 16 * ns * kWideWV - 1) / (16 * ns * kWideWV) * m_blocks * 4 < 3 * ss_host::device_cu_count()) ns = 1;
+  const int64_t n_tiles = (n + 16 * ns * kWideWV - 1) / (16 * ns * kWideWV);
   if (n_tiles > 65535 || m_blocks > 65535) return false;
   const int64_t tiles = n_tiles * m_blocks;
   const int64_t target = ss_host::device_cu_count();
@@ -2014,21 +2016,24 @@ bool plan_wide(W4Plan& pl, int64_t m, int64_t n, int64_t k, int g) {
   const int64_t rounds = stages / kWidePF;
   ks = ks < 1 ? 1 : (ks > rounds ? rounds : ks);
   int64_t per = (rounds + ks - 1) / ks * kWidePF;  // stages per range
-  while (per > kWidePF && wide_lds_bytes(kWideNS, (int)per) > kWideLdsMax) per -= kWidePF;  // the table fits
-  if (wide_lds_bytes(kWideNS, (int)per) > kWideLdsMax) return false;
-  // short ranges leave the per-workgroup set-up and result traffic uncovered: below 12
-  // stages the tiled kernel is faster (C5 at m = 256: 4096 x 6144 in 4 ranges of 8 stages
-  // 36.6 against 31.8 us, 4096 x 4096 in 8 ranges of 4 stages 32.3 against 22.0 us)
-  if (per < 12) return false;
+  while (per > kWidePF && wide_lds_bytes(ns, (int)per) > kWideLdsMax) per -= kWidePF;  // the table fits
+  if (wide_lds_bytes(ns, (int)per) > kWideLdsMax) return false;
+  ks = (stages + per - 1) / per;
+  per = (rounds + ks - 1) / ks * kWidePF;  // balanced again
+  // short ranges leave the per-workgroup set-up and result traffic uncovered: below 16
+  // stages the tiled kernel is faster (C5 at m = 256: 4096 x 6144 in 3 ranges of 12, 12
+  // and 8 stages 43.8 against 32.1 us, in 4 ranges of 8 stages 36.6 against 31.8 us;
+  // 4096 x 4096 in 8 ranges of 4 stages 32.3 against 22.0 us)
+  if (per < 16) return false;
   ks = (stages + per - 1) / per;
   if (ks > 65535) return false;
   pl.widek = true;
-  pl.mt = kWideMT, pl.ns = kWideNS;
+  pl.mt = kWideMT, pl.ns = ns;
   pl.n_tiles = (int)n_tiles;
   pl.m_blocks = (int)m_blocks;
   pl.ks = (int)ks;
   pl.kchunk = (int)per;
-  pl.lds = wide_lds_bytes(kWideNS, (int)per);
+  pl.lds = wide_lds_bytes(ns, (int)per);
   return true;
 }
 
@@ -2267,9 +2272,9 @@ int launch_w4a16_narrow_mr(const W4Params& p, const W4Plan& pl, hipStream_t stre
   return launch_w4a16_narrow_sd<T, MR, SS_DTYPE_F32>(p, pl, stream);
 }
 
-template <typename T, int SD>
+template <typename T, int NS, int SD>
 int launch_w4a16_wide_sd(const W4Params& p, const W4Plan& pl, float* part, hipStream_t stream) {
-  auto kern = w4a16_wide_kernel<T, kWideMT, kWideNS, kWideWV, SD>;
+  auto kern = w4a16_wide_kernel<T, kWideMT, NS, kWideWV, SD>;
   static bool attr_set = false;  // per instantiation; the attribute is process-wide
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLdsMax) !=
@@ -2281,7 +2286,7 @@ int launch_w4a16_wide_sd(const W4Params& p, const W4Plan& pl, float* part, hipSt
   }
   const int64_t pairs = (int64_t)pl.ks * pl.n_tiles;
   const int64_t grid = (pairs + 7) / 8 * 8 * pl.m_blocks;
-  if (grid > 0x7fffffff || pl.lds != wide_lds_bytes(kWideNS, pl.kchunk) || pl.kchunk % kWidePF) {
+  if (grid > 0x7fffffff || pl.ns != NS || pl.lds != wide_lds_bytes(NS, pl.kchunk) || pl.kchunk % kWidePF) {
     ss_host::set_error("w4a16 gemm: wide plan of %lld workgroups, %zu LDS bytes", (long long)grid, pl.lds);
     return SS_ERR_UNSUPPORTED;
   }
@@ -2309,9 +2314,14 @@ int launch_w4a16_wide_sd(const W4Params& p, const W4Plan& pl, float* part, hipSt
 template <typename T>
 int launch_w4a16_typed(const W4Params& p, const W4Plan& pl, float* part, hipStream_t stream) {
   if (pl.widek) {
-    if (p.sdt == SS_DTYPE_F16) return launch_w4a16_wide_sd<T, SS_DTYPE_F16>(p, pl, part, stream);
-    if (p.sdt == SS_DTYPE_BF16) return launch_w4a16_wide_sd<T, SS_DTYPE_BF16>(p, pl, part, stream);
-    return launch_w4a16_wide_sd<T, SS_DTYPE_F32>(p, pl, part, stream);
+    if (pl.ns == 1) {
+      if (p.sdt == SS_DTYPE_F16) return launch_w4a16_wide_sd<T, 1, SS_DTYPE_F16>(p, pl, part, stream);
+      if (p.sdt == SS_DTYPE_BF16) return launch_w4a16_wide_sd<T, 1, SS_DTYPE_BF16>(p, pl, part, stream);
+      return launch_w4a16_wide_sd<T, 1, SS_DTYPE_F32>(p, pl, part, stream);
+    }
+    if (p.sdt == SS_DTYPE_F16) return launch_w4a16_wide_sd<T, kWideNS, SS_DTYPE_F16>(p, pl, part, stream);
+    if (p.sdt == SS_DTYPE_BF16) return launch_w4a16_wide_sd<T, kWideNS, SS_DTYPE_BF16>(p, pl, part, stream);
+    return launch_w4a16_wide_sd<T, kWideNS, SS_DTYPE_F32>(p, pl, part, stream);
   }
   if (pl.narrow == 1) return launch_w4a16_narrow_mr<T, 1>(p, pl, stream);
   if (pl.narrow == 2) return launch_w4a16_narrow_mr<T, 2>(p, pl, stream);
