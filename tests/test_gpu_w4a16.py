@@ -211,19 +211,20 @@ def test_tiled_two_ranges_finished_in_kernel(device, m, n, act, sdt):
         assert torch.equal(again, y)
 
 
-# (plans as the host computes them for 256 CUs: 128 x 256 workgroup tiles, ranges of a
-# multiple of 4 stages and at least 12)
+# (plans as the host computes them for 256 CUs: 128-row activation blocks, 128- or
+# 256-row weight tiles, ranges of a multiple of 4 stages and at least 16)
 @pytest.mark.parametrize("m,k,n,act,sdt", [
-    (300, 2048, 16000, torch.float16, torch.bfloat16),   # one range; 3 M blocks (the last of 44 rows), a half last weight tile
-    (256, 3072, 16384, torch.bfloat16, torch.float16),   # two ranges of 12 stages, finished in the kernel
-    (256, 4096, 12800, torch.bfloat16, torch.float32),   # three ranges (12, 12, 8 stages) and the reduce kernel
-    (256, 3072, 16382, torch.bfloat16, torch.float16),   # two ranges, N % 4 != 0: partials and the reduce kernel
+    (300, 2048, 16000, torch.float16, torch.bfloat16),   # one range, 128-row weight tiles; 3 M blocks (the last of 44 rows)
+    (256, 2048, 28600, torch.bfloat16, torch.float32),   # one range, 256-row weight tiles, the last of 184 rows
+    (256, 4096, 8192, torch.bfloat16, torch.float16),    # two ranges of 16 stages, finished in the kernel
+    (256, 8192, 6144, torch.bfloat16, torch.float32),    # three ranges (24, 24, 16 stages) and the reduce kernel
+    (256, 4096, 8190, torch.bfloat16, torch.float16),    # two ranges, N % 4 != 0: partials and the reduce kernel
 ])
 def test_wide_kernel(device, m, k, n, act, sdt):
     """The wide kernel (m > 64, g = 128: weights dequantised once per wave with the scale
-    inside the operand, 128 x 256 workgroup tiles, activations by DMA into LDS): ragged M
-    and N, one, two and three K ranges, every scale dtype, random zero points. Within the
-    tolerance of the float64 oracle and bit-identical across repeats."""
+    inside the operand, 128 x 128 or 128 x 256 workgroup tiles, activations by DMA into
+    LDS): ragged M and N, one, two and three K ranges, every scale dtype, random zero
+    points. Within the tolerance of the float64 oracle and bit-identical across repeats."""
     print(f"w4a16 wide m={m} k={k} n={n} {act} {sdt}", flush=True)
     x, qw, s, z, ref = _host_case(n, k, m, 128, seed=m + k + n, act=act, sdt=sdt, zeros="random")
     xd, qd, sd, zd = x.to(device), qw.to(device), s.to(device), z.to(device)
@@ -239,7 +240,7 @@ def test_wide_kernel_two_ranges_graph_and_dirty_workspace(device):
     from a captured graph (one tag for every replay) to the eager result, with eager
     calls in between."""
     from slipstream_amd.kernels import quant_gemm
-    x, qw, s, z, ref = _host_case(16384, 3072, 256, 128, seed=77, zeros="random")
+    x, qw, s, z, ref = _host_case(8192, 4096, 256, 128, seed=77, zeros="random")
     xd, qd, sd, zd = x.to(device), qw.to(device), s.to(device), z.to(device)
     y = w4a16_gemm(xd, qd, sd, zd, 128)
     _assert_close(y, ref, "wide two ranges")
