@@ -219,6 +219,7 @@ def test_tiled_two_ranges_finished_in_kernel(device, m, n, act, sdt):
     (256, 4096, 8192, torch.bfloat16, torch.float16),    # two ranges of 16 stages, finished in the kernel
     (256, 8192, 6144, torch.bfloat16, torch.float32),    # three ranges (24, 24, 16 stages) and the reduce kernel
     (256, 4096, 8190, torch.bfloat16, torch.float16),    # two ranges, N % 4 != 0: partials and the reduce kernel
+    (256, 2048, 16002, torch.bfloat16, torch.float16),   # one range, N % 4 != 0: element stores of the last chunk
 ])
 def test_wide_kernel(device, m, k, n, act, sdt):
     """The wide kernel (m > 64, g = 128: weights dequantised once per wave with the scale
@@ -232,6 +233,9 @@ def test_wide_kernel(device, m, k, n, act, sdt):
     assert y.dtype == act
     _assert_close(y, ref, f"wide m={m} k={k} n={n}")
     assert torch.equal(y, w4a16_gemm(xd, qd, sd, zd, 128))
+    xs = torch.zeros(m, k + 72, dtype=act, device=device)[:, 40:40 + k]  # rows 16-byte aligned, stride k + 72
+    xs.copy_(xd)
+    assert torch.equal(w4a16_gemm(xs, qd, sd, zd, 128), y)  # strided activations: the same result
 
 
 def test_wide_kernel_two_ranges_graph_and_dirty_workspace(device):
