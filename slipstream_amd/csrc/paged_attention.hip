@@ -8,8 +8,11 @@
 
 namespace ss {
 int64_t decode_workspace_bytes(int dtype, int head_dim, int n_q, int n_kv, int max_query_len);
+// plan_work / plan_qtiles: also build the tiled prefill's work list there (one more
+// workgroup of the decode launch); *planned tells whether it did
 int launch_decode(const AttnParams& p, int dtype, int head_dim, int max_query_len, char* ws,
-                  int64_t ws_bytes, hipStream_t stream);
+                  int64_t ws_bytes, hipStream_t stream, int* plan_work = nullptr, int plan_qtiles = 0,
+                  bool* planned = nullptr);
 // shared-prefix cascade: prefix pass (pp, n_pf workgroups) and suffix decode (ps) in one
 // launch, then the merge
 int launch_cascade(const AttnParams& pp, const AttnParams& ps, int n_pf, int dtype, int head_dim, char* ws,
@@ -134,26 +137,33 @@ int run(AttnParams& p, int dtype, int head_dim, int max_query_len, void* workspa
   p.rmax = ss::decode_rows_for(max_query_len, p.n_rep);
   p.row_cap = prefill_rows ? (int)std::min<int64_t>(ss::prefill_row_cap(p.n_rep, max_query_len), 0x7fffffff) : 0;
   const int64_t dec_bytes = decode_part_bytes(dtype, head_dim, p.n_q, p.n_kv, max_query_len);
-  auto decode = [&](hipStream_t s) {
-    return ss::launch_decode(p, dtype, head_dim, max_query_len, (char*)workspace, ws_bytes, s);
+  const bool has_list = workspace && ws_bytes > dec_bytes;
+  int* const list = has_list ? (int*)((char*)workspace + dec_bytes) : nullptr;
+  auto decode = [&](hipStream_t s, int* plan_work, int plan_qtiles, bool* planned) {
+    return ss::launch_decode(p, dtype, head_dim, max_query_len, (char*)workspace, ws_bytes, s, plan_work,
+                             plan_qtiles, planned);
   };
-  auto prefill = [&](hipStream_t s) {
-    const bool has_list = workspace && ws_bytes > dec_bytes;
-    return ss::launch_prefill(p, dtype, head_dim, max_query_len, has_list ? (int*)((char*)workspace + dec_bytes) : nullptr,
-                              has_list ? ws_bytes - dec_bytes : 0, s, false);
+  auto prefill = [&](hipStream_t s, bool planned) {
+    return ss::launch_prefill(p, dtype, head_dim, max_query_len, list, has_list ? ws_bytes - dec_bytes : 0, s,
+                              planned);
   };
-  // A packed step has both kinds of rows. They run one after the other, the prefill
-  // first: each kernel fills every CU with one workgroup (registers, LDS), and the
-  // split-K decode finishes only when its last workgroup does, so sharing the GPU
-  // between them (a side stream) made whichever started second trickle in behind
-  // the first. The persistent prefill takes all CUs for its balanced share, then the
-  // decode gets all CUs at once.
+  // A packed step has both kinds of rows. They run one after the other: each kernel
+  // fills every CU with one workgroup (registers, LDS), and the split-K decode finishes
+  // only when its last workgroup does, so sharing the GPU between them (a side stream)
+  // made whichever started second trickle in behind the first. The decode goes first,
+  // with one more workgroup that builds the tiled prefill's work list beside it (when
+  // the prefill takes the tiled kernel: head_dim <= 128, blocks of >= 16 tokens); the
+  // persistent prefill then takes all CUs for its balanced share.
   if (decode_rows && prefill_rows) {
-    int st = prefill(stream);
-    return st != SS_OK ? st : decode(stream);
+    const int64_t qtiles = ((int64_t)std::max(max_query_len, 1) * p.n_rep + 127) / 128;
+    const bool tiled = head_dim <= 128 && p.block_size >= 16 && p.work_qtiles == 0 && list &&
+                       qtiles <= 0xFFFF && ws_bytes - dec_bytes >= ss::prefill_work_bytes(p.batch, p.n_rep, max_query_len);
+    bool planned = false;
+    int st = decode(stream, tiled ? list : nullptr, tiled ? (int)qtiles : 0, &planned);
+    return st != SS_OK ? st : prefill(stream, planned);
   }
-  if (decode_rows) return decode(stream);
-  if (prefill_rows) return prefill(stream);
+  if (decode_rows) return decode(stream, nullptr, 0, nullptr);
+  if (prefill_rows) return prefill(stream, false);
   return SS_OK;
 }
 

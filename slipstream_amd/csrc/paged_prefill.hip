@@ -253,65 +253,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   prefill_tile_body<T, D>(p, work, blockIdx.x, gridDim.x);
 }
 
-// Work list of the tiled prefill: work[0] = entries, work[1 + i] = (b << 16) | qt for
-// every (sequence, 128-row query tile) of a prefill sequence, ordered by decreasing
-// cost (64-key tiles below the tile's causal end, plus one): a counting sort over
-// cost buckets in LDS. Entries of equal cost land in any order; an item's result
-// does not depend on the workgroup that computes it.
-constexpr int kPlanBuckets = 1024;
+// The tiled prefill's work list (plan_work_list) built by a one-workgroup launch, when
+// no decode launch of the same call builds it.
 __global__ __launch_bounds__(1024) void prefill_plan_kernel(const AttnParams p, int* __restrict__ work,
                                                              int qtiles) {
-  __shared__ int s_hist[kPlanBuckets];
-  __shared__ int s_base[kPlanBuckets];
-  const int tid = threadIdx.x;  // blockDim.x == kPlanBuckets
-  s_hist[tid] = 0;
-  __syncthreads();
-  const int64_t n_entries = (int64_t)p.batch * qtiles;
-  // cost bucket of entry e = b * qtiles + qt, or -1 when it is not a prefill tile
-  auto bucket = [&](int64_t e) {
-    const int b = (int)(e / qtiles), qt = (int)(e - (int64_t)b * qtiles);
-    int qlen;
-    int64_t qoff;
-    seq_queries(p, b, qlen, qoff);
-    if (qlen <= 0 || is_decode_seq(p, qlen)) return -1;
-    const int R = qlen * p.n_rep, row0 = qt * 128;
-    if (row0 >= R) return -1;
-    const int ctx = kv_len(p, b);
-    const int kvt = seq_kv_tokens(p, ctx);
-    const int last_row = min(R - 1, row0 + 127);
-    const int kv_end = p.noncausal ? kvt : min(kvt, ctx - qlen + last_row / p.n_rep + 1);
-    const int cost = (kv_end > 0 ? (kv_end + 63) / 64 : 0) + 1;
-    return min(cost, kPlanBuckets - 1);
-  };
-  for (int64_t e = tid; e < n_entries; e += blockDim.x) {
-    const int c = bucket(e);
-    if (c >= 0) atomicAdd(&s_hist[c], 1);
-  }
-  __syncthreads();
-  {  // exclusive scan from the costliest bucket down: thread t takes bucket 1023 - t
-    __shared__ int s_wsum[kPlanBuckets / 64];
-    const int lane = tid & 63, wave = tid >> 6;
-    const int c = kPlanBuckets - 1 - tid;
-    int v = s_hist[c];
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int t = __shfl_up(v, o);
-      v += lane >= o ? t : 0;
-    }
-    if (lane == 63) s_wsum[wave] = v;
-    __syncthreads();
-    for (int w = 0; w < wave; ++w) v += s_wsum[w];
-    s_base[c] = v - s_hist[c];
-    if (tid == kPlanBuckets - 1) work[0] = v;
-  }
-  __syncthreads();
-  for (int64_t e = tid; e < n_entries; e += blockDim.x) {
-    const int c = bucket(e);
-    if (c >= 0) {
-      const int b = (int)(e / qtiles), qt = (int)(e - (int64_t)b * qtiles);
-      work[1 + atomicAdd(&s_base[c], 1)] = (b << 16) | qt;
-    }
-  }
+  plan_work_list(p, work, qtiles);
 }
 
 constexpr int kPrefillNT = 2;
