@@ -124,6 +124,13 @@ __device__ __forceinline__ bool is_decode_seq(const AttnParams& p, int qlen) {
   return qlen >= 1 && qlen * p.n_rep <= p.rmax;
 }
 
+// A decode launch's merge left to the next launch of the same call: the params it
+// runs with (the decode's workspace carved in) and the decode's workgroup count.
+struct DeferredMerge {
+  AttnParams p;
+  int n_wg;  // 0: nothing deferred
+};
+
 // Work list of the tiled prefill, built by one workgroup (blockDim.x a multiple of 64
 // that divides kPlanBuckets): work[0] = entries, work[1 + i] = (b << 16) | qt for every
 // (sequence, 128-row query tile) of a prefill sequence, ordered by decreasing cost

@@ -12,7 +12,10 @@ int64_t decode_workspace_bytes(int dtype, int head_dim, int n_q, int n_kv, int m
 // workgroup of the decode launch); *planned tells whether it did
 int launch_decode(const AttnParams& p, int dtype, int head_dim, int max_query_len, char* ws,
                   int64_t ws_bytes, hipStream_t stream, int* plan_work = nullptr, int plan_qtiles = 0,
-                  bool* planned = nullptr);
+                  bool* planned = nullptr, DeferredMerge* defer = nullptr);
+// the tiled prefill over a planned work list plus a deferred decode merge, one launch
+int launch_prefill_merge(const AttnParams& pp, int dtype, int head_dim, int max_query_len, const int* work,
+                         const DeferredMerge& dm, hipStream_t stream);
 // shared-prefix cascade: prefix pass (pp, n_pf workgroups) and suffix decode (ps) in one
 // launch, then the merge
 int launch_cascade(const AttnParams& pp, const AttnParams& ps, int n_pf, int dtype, int head_dim, char* ws,
@@ -139,9 +142,9 @@ int run(AttnParams& p, int dtype, int head_dim, int max_query_len, void* workspa
   const int64_t dec_bytes = decode_part_bytes(dtype, head_dim, p.n_q, p.n_kv, max_query_len);
   const bool has_list = workspace && ws_bytes > dec_bytes;
   int* const list = has_list ? (int*)((char*)workspace + dec_bytes) : nullptr;
-  auto decode = [&](hipStream_t s, int* plan_work, int plan_qtiles, bool* planned) {
+  auto decode = [&](hipStream_t s, int* plan_work, int plan_qtiles, bool* planned, ss::DeferredMerge* defer) {
     return ss::launch_decode(p, dtype, head_dim, max_query_len, (char*)workspace, ws_bytes, s, plan_work,
-                             plan_qtiles, planned);
+                             plan_qtiles, planned, defer);
   };
   auto prefill = [&](hipStream_t s, bool planned) {
     return ss::launch_prefill(p, dtype, head_dim, max_query_len, list, has_list ? ws_bytes - dec_bytes : 0, s,
@@ -159,10 +162,16 @@ int run(AttnParams& p, int dtype, int head_dim, int max_query_len, void* workspa
     const bool tiled = head_dim <= 128 && p.block_size >= 16 && p.work_qtiles == 0 && list &&
                        qtiles <= 0xFFFF && ws_bytes - dec_bytes >= ss::prefill_work_bytes(p.batch, p.n_rep, max_query_len);
     bool planned = false;
-    int st = decode(stream, tiled ? list : nullptr, tiled ? (int)qtiles : 0, &planned);
-    return st != SS_OK ? st : prefill(stream, planned);
+    ss::DeferredMerge dm{};
+    // the decode's merge then runs in the tiled prefill's launch, on the CUs its
+    // persistent workgroups leave as they finish
+    int st = decode(stream, tiled ? list : nullptr, tiled ? (int)qtiles : 0, &planned, tiled ? &dm : nullptr);
+    if (st != SS_OK) return st;
+    // (the decode defers its merge only when it also built the list)
+    if (dm.n_wg > 0) return ss::launch_prefill_merge(p, dtype, head_dim, max_query_len, list, dm, stream);
+    return prefill(stream, planned);
   }
-  if (decode_rows) return decode(stream, nullptr, 0, nullptr);
+  if (decode_rows) return decode(stream, nullptr, 0, nullptr, nullptr);
   if (prefill_rows) return prefill(stream, false);
   return SS_OK;
 }

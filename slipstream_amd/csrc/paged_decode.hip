@@ -986,10 +986,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // sequence raises kStatusPrefixShort (its suffix counts as empty). In a shared-prefix
 // call the merge also folds the prefix parts into the rows it writes.
 template <typename T, int D>
-__global__ __launch_bounds__(512) void decode_merge_kernel(const AttnParams p, int n_wg, int n_fin) {
+__device__ __forceinline__ void decode_merge_body(const AttnParams& p, const int n_wg, const int n_fin, const int blk) {
   const int tid = threadIdx.x;
-  if ((int)blockIdx.x >= n_wg + n_fin) {
-    const int b = blockIdx.x - n_wg - n_fin;
+  if (blk >= n_wg + n_fin) {
+    const int b = blk - n_wg - n_fin;
     int qlen;
     int64_t qoff;
     seq_queries(p, b, qlen, qoff);
@@ -1039,9 +1039,9 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const AttnParams p, i
     return;
   }
   if constexpr (D <= 128) {
-    if ((int)blockIdx.x >= n_wg) {  // n_fin > 0: shared-prefix cascade
-      const int* rec = p.ws_rec + (int64_t)(blockIdx.x - n_wg) * 8;
-      const int hg = (blockIdx.x - n_wg) % p.n_hgroups;
+    if (blk >= n_wg) {  // n_fin > 0: shared-prefix cascade
+      const int* rec = p.ws_rec + (int64_t)(blk - n_wg) * 8;
+      const int hg = (blk - n_wg) % p.n_hgroups;
       const int c0 = rec[5], c1 = rec[6];
       if (c0 >= 0) {
         // shared-prefix cascade: the sequences this range finished (one query token
@@ -1074,12 +1074,12 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const AttnParams p, i
       return;
     }
   }
-  const int* rec = p.ws_rec + (int64_t)blockIdx.x * 8;
-  const int hg = blockIdx.x % p.n_hgroups;
+  const int* rec = p.ws_rec + (int64_t)blk * 8;
+  const int hg = blk % p.n_hgroups;
   const int b = rec[0];
   if (b < 0) return;
   const int cb1 = rec[2], slot0 = rec[3], chunk = rec[4];
-  const int wr0 = blockIdx.x / p.n_hgroups;
+  const int wr0 = blk / p.n_hgroups;
   const int wr1 = (cb1 - 1) / chunk;
   int qlen;
   int64_t qoff;
@@ -1148,6 +1148,25 @@ __global__ __launch_bounds__(512) void decode_merge_kernel(const AttnParams p, i
   }
 }
 
+template <typename T, int D>
+__global__ __launch_bounds__(512) void decode_merge_kernel(const AttnParams p, int n_wg, int n_fin) {
+  decode_merge_body<T, D>(p, n_wg, n_fin, blockIdx.x);
+}
+
+// A packed call's tiled prefill (pp, workgroups [0, n_pf) walking the work list) and
+// the merge of its decode (pm, the others) in one launch, after the decode launch: the
+// two write disjoint rows. The persistent prefill's workgroups finish unevenly (the
+// costliest items set the tail) and the merge blocks take the CUs they leave, instead
+// of a launch of their own before or after the prefill.
+template <typename T, int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_merge_kernel(
+    const AttnParams pp, const int* __restrict__ work, const int n_pf, const AttnParams pm, const int n_wg) {
+  if ((int)blockIdx.x < n_pf)
+    prefill_tile_body<T, D>(pp, work, blockIdx.x, n_pf);
+  else
+    decode_merge_body<T, D>(pm, n_wg, 0, blockIdx.x - n_pf);
+}
+
 }  // namespace
 
 // ---- host side -------------------------------------------------------------
@@ -1214,8 +1233,10 @@ int64_t decode_workspace_bytes(int dtype, int head_dim, int n_q, int n_kv, int m
 
 template <typename T, int D>
 static int launch_decode_typed(AttnParams p, int max_query_len, char* ws, int64_t ws_bytes,
-                               hipStream_t stream, int* plan_work, int plan_qtiles, bool* planned) {
+                               hipStream_t stream, int* plan_work, int plan_qtiles, bool* planned,
+                               DeferredMerge* defer) {
   if (planned) *planned = false;
+  if (defer) defer->n_wg = 0;
   const DecodeGeometry g = decode_geometry<T, D>(p.n_kv, decode_rows_for(max_query_len, p.n_rep));
   if (ws_bytes < g.total()) {
     ss_host::set_error("paged attention: workspace of %lld bytes, decode needs %lld", (long long)ws_bytes,
@@ -1277,6 +1298,13 @@ static int launch_decode_typed(AttnParams p, int max_query_len, char* ws, int64_
                        p);
   int st = ss_host::launch_status("paged attention decode");
   if (st != SS_OK) return st;
+  // the merge left to the caller's next launch (a packed call's prefill, which then
+  // runs it in its spare workgroups); the call's params with the decode's workspace
+  if (defer && plan && p.block_size >= 16 && D <= 128 && p.px_n == 0) {  // only with the list built
+    defer->p = p;
+    defer->n_wg = n_wg;
+    return SS_OK;
+  }
   // a shared-prefix merge folds S prefix parts into each of its rows' 8-d pieces (28 x
   // 16 per C4 sequence): 512 threads give every piece its own thread
   const int merge_threads = p.px_n > 0 ? 512 : 256;
@@ -1389,22 +1417,65 @@ int launch_cascade(const AttnParams& pp, const AttnParams& ps, int n_pf, int dty
   return launch_cascade_typed<f16_t, 256>(pp, ps, n_pf, ws, ws_bytes, stream);
 }
 
+// A packed call's tiled prefill (pp over the work list) together with the decode merge
+// deferred by launch_decode (dm), in one launch: prefill_merge_kernel.
+template <typename T, int D>
+static int launch_prefill_merge_typed(const AttnParams& pp, int max_query_len, const int* work,
+                                      const DeferredMerge& dm, hipStream_t stream) {
+  const int64_t qtiles = ((int64_t)(max_query_len < 1 ? 1 : max_query_len) * pp.n_rep + 127) / 128;
+  const int64_t items = (int64_t)pp.batch * qtiles * pp.n_kv;
+  const int64_t cus = ss_host::device_cu_count();
+  const int n_pf = (int)(items < cus ? items : cus);
+  const int64_t grid = (int64_t)n_pf + dm.n_wg + dm.p.batch;
+  if (grid > 0x7fffffff || n_pf < 1) {
+    ss_host::set_error("paged attention: prefill + merge grid of %lld workgroups", (long long)grid);
+    return SS_ERR_UNSUPPORTED;
+  }
+  const int lds = 6 * TileCfg<T, D>::PLANE;  // the prefill's K and V rings
+  static bool attr_set = false;  // per instantiation; the attribute is process-wide
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)prefill_merge_kernel<T, D>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            lds) != hipSuccess) {
+      ss_host::set_error("paged attention prefill + merge: cannot reserve %d bytes of LDS", lds);
+      return SS_ERR_UNSUPPORTED;
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((prefill_merge_kernel<T, D>), dim3((unsigned)grid), dim3(512), lds, stream, pp, work, n_pf, dm.p,
+                     dm.n_wg);
+  return ss_host::launch_status("paged attention prefill + decode merge");
+}
+
+int launch_prefill_merge(const AttnParams& pp, int dtype, int head_dim, int max_query_len, const int* work,
+                         const DeferredMerge& dm, hipStream_t stream) {
+  if (head_dim > 128 || pp.block_size < 16 || !work || dm.n_wg < 1) {
+    ss_host::set_error("paged attention prefill + merge: head_dim %d, block size %d", head_dim, pp.block_size);
+    return SS_ERR_UNSUPPORTED;
+  }
+  if (dtype == SS_DTYPE_BF16)
+    return head_dim == 64 ? launch_prefill_merge_typed<bf16_t, 64>(pp, max_query_len, work, dm, stream)
+                          : launch_prefill_merge_typed<bf16_t, 128>(pp, max_query_len, work, dm, stream);
+  return head_dim == 64 ? launch_prefill_merge_typed<f16_t, 64>(pp, max_query_len, work, dm, stream)
+                        : launch_prefill_merge_typed<f16_t, 128>(pp, max_query_len, work, dm, stream);
+}
+
 int launch_decode(const AttnParams& p, int dtype, int head_dim, int max_query_len, char* ws,
-                  int64_t ws_bytes, hipStream_t stream, int* plan_work, int plan_qtiles, bool* planned) {
+                  int64_t ws_bytes, hipStream_t stream, int* plan_work, int plan_qtiles, bool* planned,
+                  DeferredMerge* defer) {
   if (dtype == SS_DTYPE_BF16) {
     if (head_dim == 64) return launch_decode_typed<bf16_t, 64>(p, max_query_len, ws, ws_bytes, stream, plan_work,
-                                                   plan_qtiles, planned);
+                                                   plan_qtiles, planned, defer);
     if (head_dim == 128) return launch_decode_typed<bf16_t, 128>(p, max_query_len, ws, ws_bytes, stream, plan_work,
-                                                   plan_qtiles, planned);
+                                                   plan_qtiles, planned, defer);
     return launch_decode_typed<bf16_t, 256>(p, max_query_len, ws, ws_bytes, stream, plan_work,
-                                                   plan_qtiles, planned);
+                                                   plan_qtiles, planned, defer);
   }
   if (head_dim == 64) return launch_decode_typed<f16_t, 64>(p, max_query_len, ws, ws_bytes, stream, plan_work,
-                                                   plan_qtiles, planned);
+                                                   plan_qtiles, planned, defer);
   if (head_dim == 128) return launch_decode_typed<f16_t, 128>(p, max_query_len, ws, ws_bytes, stream, plan_work,
-                                                   plan_qtiles, planned);
+                                                   plan_qtiles, planned, defer);
   return launch_decode_typed<f16_t, 256>(p, max_query_len, ws, ws_bytes, stream, plan_work,
-                                                   plan_qtiles, planned);
+                                                   plan_qtiles, planned, defer);
 }
 
 }  // namespace ss
