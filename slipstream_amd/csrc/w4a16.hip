@@ -1004,8 +1004,13 @@ __global__ __launch_bounds__(64 * WV) void w4a16_wide_kernel(const W4Params p, f
 #pragma unroll
   for (int ns = 0; ns < NS; ++ns) w_off[ns] = min(n0 + ns * 16 + ln, p.n - 1) * (p.k / 2) + 16 * kg;
   u32x4 wr[PF][NS];
+  // The loads are asm, so the compiler's hazard recognizer does not see them read the
+  // offset SGPR: a VALU write of an SGPR (v_readfirstlane) needs five wait states before
+  // a VMEM instruction reads it. The s_nop, ordered after the offset's computation by its
+  // operand and before the loads as a volatile asm, keeps them whatever the schedule.
   auto load_w = [&](int i, u32x4 (&w)[NS]) {
     const int so = __builtin_amdgcn_readfirstlane(i < i1 ? i * 64 : kOutOfRange);
+    asm volatile("s_nop 4" : : "s"(so));
 #pragma unroll
     for (int ns = 0; ns < NS; ++ns) w[ns] = asm_load_b128_nt(rw, w_off[ns], so);
   };
@@ -1024,6 +1029,7 @@ __global__ __launch_bounds__(64 * WV) void w4a16_wide_kernel(const W4Params p, f
   const LdsW lds_x = (LdsW)s_dyn;
   auto dma_x = [&](int i, int buf) {
     const int so = __builtin_amdgcn_readfirstlane(i < i1 ? i * 128 * (int)sizeof(T) : kOutOfRange);
+    asm volatile("s_nop 4" : : "s"(so));  // as in load_w
 #pragma unroll
     for (int u = 0; u < XI; ++u) asm_dma_b128(rx, lds_x + buf * XBYTES + (XI * wave + u) * 1024, x_off[u], so);
   };
