@@ -159,8 +159,10 @@ int run(AttnParams& p, int dtype, int head_dim, int max_query_len, void* workspa
   // persistent prefill then takes all CUs for its balanced share.
   if (decode_rows && prefill_rows) {
     const int64_t qtiles = ((int64_t)std::max(max_query_len, 1) * p.n_rep + 127) / 128;
-    const bool tiled = head_dim <= 128 && p.block_size >= 16 && p.work_qtiles == 0 && list &&
-                       qtiles <= 0xFFFF && ws_bytes - dec_bytes >= ss::prefill_work_bytes(p.batch, p.n_rep, max_query_len);
+    // (the list's entries are (b << 16) | query tile: the limits the prefill launch checks)
+    const bool tiled = head_dim <= 128 && p.block_size >= 16 && p.work_qtiles == 0 && list && qtiles <= 0xFFFF &&
+                       p.batch <= 0x7FFF && (int64_t)p.batch * qtiles * p.n_kv <= 0x7fffffff &&
+                       ws_bytes - dec_bytes >= ss::prefill_work_bytes(p.batch, p.n_rep, max_query_len);
     bool planned = false;
     ss::DeferredMerge dm{};
     // the decode's merge then runs in the tiled prefill's launch, on the CUs its
