@@ -932,9 +932,10 @@ __device__ __forceinline__ void vm_wait_tied(u32x4 (&w)[NS]) {
 
 // Wide kernel (w4a16_wide_kernel, m > 64 and g == 128): the weights dequantised once
 // per wave into bf16/fp16 MFMA operands, each serving a whole 128-row activation tile.
-// Workgroup: four waves, 16*MT activation rows x 64*NS weight rows; wave w owns the
-// weight rows [nb + 16 NS w, + 16 NS) against every activation row of the tile, so no
-// weight is dequantised twice inside a workgroup. Per 128-key stage (one quantisation
+// Workgroup: WV waves (eight: two per SIMD, so one wave's MFMAs run beside the other's
+// dequantisation), 16*MT activation rows x 16*NS*WV weight rows; wave w owns the weight
+// rows [nb + 16 NS w, + 16 NS) against every activation row of the tile, so no weight is
+// dequantised twice inside a workgroup. Per 128-key stage (one quantisation
 // group):
 //   - each lane loads its 32 keys of each of its NS weight rows (one 16-byte load per
 //     16-row tile, four lanes reading a row's 64 contiguous bytes) PF stages ahead (a
